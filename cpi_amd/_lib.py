@@ -1,0 +1,111 @@
+"""ctypes binding of the C-ABI in include/cpi_hip.h (libcpi_hip.so).
+
+The library is built in-tree by cpi_amd.build; loading fails loudly if it is
+missing — there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libcpi_hip.so")
+ENGINE_PATH = os.path.join(_HERE, "libcpi_engine.so")
+
+_lib = None
+_eng = None
+
+c_int, c_float, c_void_p, c_size_t = ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+c_int_p = ctypes.POINTER(ctypes.c_int)
+
+
+class GemvDesc(ctypes.Structure):
+    """Mirror of cpi_gemv_desc."""
+    _fields_ = [
+        ("wfmt", c_int), ("w", c_void_p), ("scales", c_void_p), ("scale_count", c_int),
+        ("out_features", c_int), ("in_features", c_int), ("x", c_void_p), ("x_is_f32", c_int),
+        ("norm_w", c_void_p), ("norm_eps", c_float), ("epilogue", c_int), ("y", c_void_p),
+        ("num_heads", c_int), ("num_kv_heads", c_int), ("head_dim", c_int), ("position", c_void_p),
+        ("rope_cos", c_void_p), ("rope_sin", c_void_p), ("k_cache", c_void_p), ("v_cache", c_void_p),
+        ("max_context", c_int),
+    ]
+
+
+W_F16, W_I8ROW, W_I4ROW, W_I4G32 = 0, 1, 2, 3
+EPI_STORE_F32, EPI_STORE_F16, EPI_RESID_ADD, EPI_SWIGLU, EPI_QKV_ROPE = 0, 1, 2, 3, 4
+ATTN_MAX_SPLITS = 256
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "cpi_hip_last_error_string": (ctypes.c_char_p, []),
+    "cpi_hip_version": (c_int, []),
+    "cpi_hip_can_fit_on_device": (c_int, [c_size_t, c_size_t]),
+    "cpi_hip_weight_only_int4_matvec": (c_int, [c_void_p] * 4 + [c_int, c_int, c_void_p]),
+    "cpi_hip_weight_only_int4g32_matvec": (c_int, [c_void_p] * 4 + [c_int, c_int, c_void_p]),
+    "cpi_hip_weight_only_int8_matvec": (c_int, [c_void_p] * 4 + [c_int, c_int, c_void_p]),
+    "cpi_hip_rowmajor_half_gemv_f16": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p]),
+    "cpi_hip_rowmajor_half_gemv_f32": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p]),
+    "cpi_hip_weight_only_dual_matvec": (c_int, [c_int] + [c_void_p] * 7 + [c_int, c_int, c_void_p]),
+    "cpi_hip_gemv": (c_int, [ctypes.POINTER(GemvDesc), c_void_p]),
+    "cpi_hip_qkv_row_order": (c_int, [c_int, c_int, c_int, c_int_p]),
+    "cpi_hip_swiglu_row_order": (c_int, [c_int, c_int_p]),
+    "cpi_hip_gather_rows": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_size_t, c_void_p]),
+    "cpi_hip_attention_scratch_floats": (c_size_t, [c_int, c_int]),
+    "cpi_hip_attention_decode": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int,
+                                         c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "cpi_hip_attention_step": (c_int, [c_void_p] * 4 + [c_int] * 4 + [c_void_p, c_void_p]),
+    "cpi_hip_attention_step_device_pos": (c_int, [c_void_p] * 5 + [c_int] * 4 + [c_void_p, c_void_p]),
+    "cpi_hip_attention_prefill": (c_int, [c_void_p] * 4 + [c_int] * 5 + [c_void_p]),
+    "cpi_hip_rmsnorm": (c_int, [c_void_p] * 3 + [c_int, c_int, c_float, c_void_p]),
+    "cpi_hip_embedding_lookup": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p]),
+    "cpi_hip_embedding_lookup_f32": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p]),
+    "cpi_hip_rope_inplace_table": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p,
+                                           c_void_p, c_void_p]),
+    "cpi_hip_rope_inplace_device_pos": (c_int, [c_void_p, c_void_p, c_int, c_int, c_int, c_void_p,
+                                                c_void_p, c_void_p, c_void_p]),
+    "cpi_rope_tables": (c_int, [c_int, c_int, c_float, c_void_p, c_void_p]),
+    "cpi_hip_store_kv_device_pos": (c_int, [c_void_p] * 5 + [c_int, c_int, c_void_p]),
+    "cpi_hip_copy_int": (c_int, [c_void_p, c_void_p, c_void_p]),
+    "cpi_hip_increment_int": (c_int, [c_void_p, c_void_p]),
+    "cpi_hip_add_inplace": (c_int, [c_void_p, c_void_p, c_int, c_void_p]),
+    "cpi_hip_silu_mul": (c_int, [c_void_p] * 3 + [c_int, c_void_p]),
+    "cpi_hip_scale_copy": (c_int, [c_void_p, c_void_p, c_int, c_float, c_void_p]),
+    "cpi_hip_scale_add_inplace": (c_int, [c_void_p, c_void_p, c_int, c_float, c_void_p]),
+    "cpi_hip_moe_router_topk_softmax": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "cpi_hip_argmax_float": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
+    "cpi_hip_quantize_rowwise_fp16_to_int8": (c_int, [c_void_p] * 3 + [c_int, c_int, c_int, c_void_p]),
+    "cpi_hip_pack_rowwise_int8_to_int4": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
+    "cpi_hip_dequant_rowwise_int8_to_fp16": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p]),
+    "cpi_hip_unpack_int4_to_int8": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
+}
+
+
+class CpiHipError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load libcpi_hip.so (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise CpiHipError(f"{LIB_PATH} is missing: run __graft_entry__.build() (no CPU fallback exists)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def declared_symbols():
+    return list(_SIGS)
+
+
+def call(name: str, *args) -> int:
+    """Call an int-returning entry point and raise on a non-zero status."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise CpiHipError(f"{name} -> {rc}: {lib().cpi_hip_last_error_string().decode(errors='replace')}")
+    return rc

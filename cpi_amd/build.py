@@ -1,0 +1,61 @@
+"""In-tree build of the native libraries (hipcc, gfx950).
+
+    libcpi_hip.so     kernels + C-ABI (include/cpi_hip.h)
+    libcpi_engine.so  C++ decode engine over the C-ABI (include/cpi_engine.h)
+    llama_infer       CLI (same flags as the reference's llama_infer)
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-Wno-unused-variable", "-Wno-unused-command-line-argument"]
+
+
+def _run(cmd):
+    print("[build]", " ".join(cmd), flush=True)
+    r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    out = "\n".join(l for l in r.stdout.splitlines() if "packed-fp32-ops" not in l)
+    if out.strip():
+        print(out)
+    if r.returncode != 0:
+        raise RuntimeError(f"build step failed ({r.returncode}): {' '.join(cmd)}")
+
+
+def build_hip():
+    src = os.path.join(HERE, "csrc", "capi.hip")
+    _run([HIPCC, *HIP_FLAGS, "-shared", src, "-o", os.path.join(HERE, "libcpi_hip.so")])
+
+
+def build_engine():
+    edir = os.path.join(HERE, "engine")
+    if not os.path.isdir(edir):
+        return
+    srcs = sorted(os.path.join(edir, f) for f in os.listdir(edir) if f.endswith(".cpp") and f != "main.cpp")
+    if not srcs:
+        return
+    inc = ["-I", os.path.join(ROOT, "include"), "-I", edir]
+    lib = os.path.join(HERE, "libcpi_engine.so")
+    link = ["-L", HERE, "-lcpi_hip", "-Wl,-rpath,$ORIGIN"]
+    _run([HIPCC, *HIP_FLAGS, *inc, "-shared", *srcs, "-o", lib, *link])
+    main = os.path.join(edir, "main.cpp")
+    if os.path.exists(main):
+        _run([HIPCC, *HIP_FLAGS, *inc, main, "-o", os.path.join(HERE, "llama_infer"),
+              "-L", HERE, "-lcpi_engine", "-lcpi_hip", "-Wl,-rpath,$ORIGIN"])
+
+
+def build_all():
+    build_hip()
+    build_engine()
+
+
+if __name__ == "__main__":
+    build_all()
+    sys.exit(0)

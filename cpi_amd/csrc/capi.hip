@@ -1,0 +1,384 @@
+// C-ABI of the gfx950 decode kernels (declared in include/cpi_hip.h).
+//
+// Single translation unit: the kernel sources are included here so that the
+// shared library is built by one hipcc invocation without relocatable device
+// code.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "gemv.hip"
+#include "attention.hip"
+#include "ops.hip"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const std::string& msg) {
+  g_last_error = msg;
+  return CPI_HIP_EINVAL;
+}
+
+int check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return 0;
+  g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+  return static_cast<int>(e);
+}
+
+hipStream_t S(cpi_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+int grid_for(size_t n, int block) {
+  size_t g = (n + block - 1) / block;
+  if (g < 1) g = 1;
+  if (g > 4096) g = 4096;
+  return static_cast<int>(g);
+}
+
+int gemv_common(int wfmt, int epi, const void* w, const void* scales, int scale_count,
+                const void* x, bool xf32, void* y, int R, int K, hipStream_t s,
+                const char* who) {
+  if (!w || !x || !y || R <= 0 || K <= 0) return fail(std::string(who) + ": null pointer or empty shape");
+  const int ce = cpi::gemv_elems_per_chunk(wfmt);
+  if (ce == 0) return fail(std::string(who) + ": unknown weight format");
+  if (K % ce != 0)
+    return fail(std::string(who) + ": in_features must be a multiple of " + std::to_string(ce));
+  if ((reinterpret_cast<uintptr_t>(w) & 15) != 0) return fail(std::string(who) + ": weights not 16-byte aligned");
+  if (wfmt != CPI_W_F16 && !scales) return fail(std::string(who) + ": missing scales");
+  cpi::GemvParams p{};
+  p.w = w;
+  p.scales = scales;
+  p.scale_count = scale_count;
+  p.R = R;
+  p.K = K;
+  p.x = x;
+  p.y = y;
+  return check(cpi::gemv_launch(wfmt, epi, xf32, p, s), who);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* cpi_hip_last_error_string(void) { return g_last_error.c_str(); }
+int cpi_hip_version(void) { return 1; }
+
+int cpi_hip_can_fit_on_device(size_t bytes, size_t margin) {
+  size_t free_b = 0, total_b = 0;
+  if (hipMemGetInfo(&free_b, &total_b) != hipSuccess) return 0;
+  return free_b >= bytes + margin ? 1 : 0;
+}
+
+// ---------------------------------------------------------------- GEMV
+int cpi_hip_weight_only_int4_matvec(const int8_t* w, const float* scales, const uint16_t* x,
+                                    uint16_t* y, int R, int K, cpi_stream_t s) {
+  return gemv_common(CPI_W_I4ROW, CPI_EPI_STORE_F16, w, scales, R, x, false, y, R, K, S(s),
+                     "weight_only_int4_matvec");
+}
+int cpi_hip_weight_only_int4g32_matvec(const int8_t* w, const uint16_t* gs, const uint16_t* x,
+                                       uint16_t* y, int R, int K, cpi_stream_t s) {
+  return gemv_common(CPI_W_I4G32, CPI_EPI_STORE_F16, w, gs, R * (K / 32), x, false, y, R, K,
+                     S(s), "weight_only_int4g32_matvec");
+}
+int cpi_hip_weight_only_int8_matvec(const int8_t* w, const float* scales, const uint16_t* x,
+                                    uint16_t* y, int R, int K, cpi_stream_t s) {
+  return gemv_common(CPI_W_I8ROW, CPI_EPI_STORE_F16, w, scales, R, x, false, y, R, K, S(s),
+                     "weight_only_int8_matvec");
+}
+int cpi_hip_rowmajor_half_gemv_f16(const uint16_t* w, const uint16_t* x, uint16_t* y, int R,
+                                   int K, cpi_stream_t s) {
+  return gemv_common(CPI_W_F16, CPI_EPI_STORE_F16, w, nullptr, 0, x, false, y, R, K, S(s),
+                     "rowmajor_half_gemv_f16");
+}
+int cpi_hip_rowmajor_half_gemv_f32(const uint16_t* w, const uint16_t* x, float* y, int R, int K,
+                                   cpi_stream_t s) {
+  return gemv_common(CPI_W_F16, CPI_EPI_STORE_F32, w, nullptr, 0, x, false, y, R, K, S(s),
+                     "rowmajor_half_gemv_f32");
+}
+
+int cpi_hip_weight_only_dual_matvec(int wfmt, const void* w_a, const void* sa, const void* w_b,
+                                    const void* sb, const uint16_t* x, uint16_t* y_a,
+                                    uint16_t* y_b, int R, int K, cpi_stream_t s) {
+  // Two launches of the same kernel; x preparation is per workgroup anyway.
+  const int sc = (wfmt == CPI_W_I4G32) ? R * (K / 32) : R;
+  int rc = gemv_common(wfmt, CPI_EPI_STORE_F16, w_a, sa, sc, x, false, y_a, R, K, S(s),
+                       "weight_only_dual_matvec(a)");
+  if (rc) return rc;
+  return gemv_common(wfmt, CPI_EPI_STORE_F16, w_b, sb, sc, x, false, y_b, R, K, S(s),
+                     "weight_only_dual_matvec(b)");
+}
+
+int cpi_hip_gemv(const cpi_gemv_desc* d, cpi_stream_t s) {
+  if (!d) return fail("gemv: null descriptor");
+  const int ce = cpi::gemv_elems_per_chunk(d->wfmt);
+  if (ce == 0) return fail("gemv: unknown weight format");
+  if (!d->w || !d->x || !d->y || d->out_features <= 0 || d->in_features <= 0)
+    return fail("gemv: null pointer or empty shape");
+  if (d->in_features % ce != 0)
+    return fail("gemv: in_features must be a multiple of " + std::to_string(ce));
+  if ((reinterpret_cast<uintptr_t>(d->w) & 15) != 0) return fail("gemv: weights not 16-byte aligned");
+  if (d->wfmt != CPI_W_F16 && !d->scales) return fail("gemv: missing scales");
+  if (d->wfmt == CPI_W_I8ROW || d->wfmt == CPI_W_I4ROW) {
+    if (d->scale_count != 1 && d->scale_count != d->out_features)
+      return fail("gemv: scale_count must be 1 or out_features");
+  }
+  cpi::GemvParams p{};
+  p.w = d->w;
+  p.scales = d->scales;
+  p.scale_count = d->scale_count;
+  p.R = d->out_features;
+  p.K = d->in_features;
+  p.x = d->x;
+  p.norm_w = d->norm_w;
+  p.eps = d->norm_eps;
+  p.y = d->y;
+  if (d->epilogue == CPI_EPI_SWIGLU && (d->out_features % 8) != 0)
+    return fail("gemv: SWIGLU needs out_features (= 2 x intermediate) % 8 == 0");
+  if (d->epilogue == CPI_EPI_QKV_ROPE) {
+    if (d->head_dim % 8 != 0 || d->num_heads <= 0 || d->num_kv_heads <= 0)
+      return fail("gemv: QKV_ROPE needs head_dim % 8 == 0 and positive head counts");
+    if (d->out_features != (d->num_heads + 2 * d->num_kv_heads) * d->head_dim)
+      return fail("gemv: QKV_ROPE out_features != (nh + 2 nkv) * head_dim");
+    if (!d->position || !d->rope_cos || !d->rope_sin || !d->k_cache || !d->v_cache)
+      return fail("gemv: QKV_ROPE needs position, rope tables and KV cache");
+    p.nh = d->num_heads;
+    p.nkv = d->num_kv_heads;
+    p.hd = d->head_dim;
+    p.position = d->position;
+    p.rope_cos = d->rope_cos;
+    p.rope_sin = d->rope_sin;
+    p.k_cache = d->k_cache;
+    p.v_cache = d->v_cache;
+    p.max_ctx = d->max_context;
+  }
+  if (d->epilogue < CPI_EPI_STORE_F32 || d->epilogue > CPI_EPI_QKV_ROPE)
+    return fail("gemv: unknown epilogue");
+  return check(cpi::gemv_launch(d->wfmt, d->epilogue, d->x_is_f32 != 0, p, S(s)), "gemv");
+}
+
+int cpi_hip_qkv_row_order(int nh, int nkv, int hd, int* out) {
+  if (!out || hd % 8 != 0 || nh <= 0 || nkv <= 0) return fail("qkv_row_order: bad shape");
+  const int half = hd / 2;
+  int i = 0;
+  for (int region = 0; region < 2; ++region) {
+    const int heads = region == 0 ? nh : nkv;
+    const int base = region == 0 ? 0 : nh * hd;
+    for (int h = 0; h < heads; ++h)
+      for (int b = 0; b < hd / 8; ++b) {
+        for (int r = 0; r < 4; ++r) out[i++] = base + h * hd + 4 * b + r;
+        for (int r = 0; r < 4; ++r) out[i++] = base + h * hd + half + 4 * b + r;
+      }
+  }
+  const int vbase = (nh + nkv) * hd;
+  for (int r = 0; r < nkv * hd; ++r) out[i++] = vbase + r;
+  return 0;
+}
+
+int cpi_hip_swiglu_row_order(int inter, int* out) {
+  if (!out || inter <= 0 || inter % 4 != 0) return fail("swiglu_row_order: intermediate % 4 != 0");
+  int i = 0;
+  for (int t = 0; t < inter / 4; ++t) {
+    for (int r = 0; r < 4; ++r) out[i++] = 4 * t + r;          // w1 rows
+    for (int r = 0; r < 4; ++r) out[i++] = inter + 4 * t + r;  // w3 rows
+  }
+  return 0;
+}
+
+int cpi_hip_gather_rows(const void* src, void* dst, const int* idx, int rows, size_t row_bytes,
+                        cpi_stream_t s) {
+  if (!src || !dst || !idx || rows <= 0) return fail("gather_rows: bad arguments");
+  hipLaunchKernelGGL(cpi::gather_rows_kernel, dim3(rows), dim3(256), 0, S(s),
+                     static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), idx, rows,
+                     row_bytes);
+  return check(hipGetLastError(), "gather_rows");
+}
+
+// ------------------------------------------------------------ attention
+size_t cpi_hip_attention_scratch_floats(int nh, int hd) {
+  return static_cast<size_t>(nh) * CPI_ATTN_MAX_SPLITS * (hd + 2);
+}
+
+int cpi_hip_attention_decode(const void* q, int q_is_f32, const uint16_t* k, const uint16_t* v,
+                             void* out, int out_is_f32, int seq_len, const int* position, int nh,
+                             int nkv, int hd, int max_ctx, int window, float* scratch,
+                             cpi_stream_t s) {
+  if (!q || !k || !v || !out || !scratch) return fail("attention_decode: null pointer");
+  if (!cpi::attn_supported(nh, nkv, hd))
+    return fail("attention_decode: supported shapes are head_dim 64/128 and nh/nkv in {1,2,4,8}");
+  if (!position && (seq_len <= 0 || seq_len > max_ctx))
+    return fail("attention_decode: seq_len must be in [1, max_context]");
+  return check(cpi::attn_launch(q, q_is_f32 != 0, k, v, out, out_is_f32 != 0, seq_len, position,
+                                nh, nkv, hd, max_ctx, window, scratch, S(s)),
+               "attention_decode");
+}
+
+int cpi_hip_attention_step(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                           int seq_len, int nh, int nkv, int hd, float* scratch, cpi_stream_t s) {
+  return cpi_hip_attention_decode(q, 0, k, v, out, 0, seq_len, nullptr, nh, nkv, hd, seq_len, 0,
+                                  scratch, s);
+}
+
+int cpi_hip_attention_step_device_pos(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                      uint16_t* out, const int* position, int nh, int nkv, int hd,
+                                      int max_ctx, float* scratch, cpi_stream_t s) {
+  if (!position) return fail("attention_step_device_pos: null position");
+  return cpi_hip_attention_decode(q, 0, k, v, out, 0, 0, position, nh, nkv, hd, max_ctx, 0,
+                                  scratch, s);
+}
+
+// ------------------------------------------------------------ small ops
+int cpi_hip_rmsnorm(const uint16_t* x, const uint16_t* w, uint16_t* y, int rows, int cols,
+                    float eps, cpi_stream_t s) {
+  if (!x || !w || !y || rows <= 0 || cols <= 0) return fail("rmsnorm: bad arguments");
+  hipLaunchKernelGGL(cpi::rmsnorm_kernel, dim3(rows), dim3(256), 0, S(s), x, w, y, cols, eps);
+  return check(hipGetLastError(), "rmsnorm");
+}
+
+int cpi_hip_embedding_lookup(const uint16_t* emb, const int* ids, uint16_t* out, int n, int hidden,
+                             cpi_stream_t s) {
+  if (!emb || !ids || !out || n <= 0 || hidden <= 0) return fail("embedding_lookup: bad arguments");
+  hipLaunchKernelGGL(cpi::embedding_kernel<false>, dim3(n), dim3(256), 0, S(s), emb, ids,
+                     static_cast<void*>(out), hidden);
+  return check(hipGetLastError(), "embedding_lookup");
+}
+
+int cpi_hip_embedding_lookup_f32(const uint16_t* emb, const int* ids, float* out, int n,
+                                 int hidden, cpi_stream_t s) {
+  if (!emb || !ids || !out || n <= 0 || hidden <= 0) return fail("embedding_lookup_f32: bad arguments");
+  hipLaunchKernelGGL(cpi::embedding_kernel<true>, dim3(n), dim3(256), 0, S(s), emb, ids,
+                     static_cast<void*>(out), hidden);
+  return check(hipGetLastError(), "embedding_lookup_f32");
+}
+
+static int rope_common(uint16_t* q, uint16_t* k, int nq, int nk, int hd, int pos, const int* pd,
+                       const float* c, const float* sn, hipStream_t s) {
+  if (!q || !k || !c || !sn || hd <= 0 || (hd & 1) || hd / 2 > 1024) return fail("rope: bad arguments");
+  hipLaunchKernelGGL(cpi::rope_kernel, dim3(nq > nk ? nq : nk), dim3(hd / 2), 0, s, q, k, nq, nk,
+                     hd, pos, pd, c, sn);
+  return check(hipGetLastError(), "rope");
+}
+
+int cpi_hip_rope_inplace_table(uint16_t* q, uint16_t* k, int nq, int nk, int hd, int pos,
+                               const float* c, const float* sn, cpi_stream_t s) {
+  return rope_common(q, k, nq, nk, hd, pos, nullptr, c, sn, S(s));
+}
+int cpi_hip_rope_inplace_device_pos(uint16_t* q, uint16_t* k, int nq, int nk, int hd,
+                                    const int* pos, const float* c, const float* sn,
+                                    cpi_stream_t s) {
+  if (!pos) return fail("rope_device_pos: null position");
+  return rope_common(q, k, nq, nk, hd, 0, pos, c, sn, S(s));
+}
+
+int cpi_rope_tables(int max_ctx, int hd, float theta, float* cos_out, float* sin_out) {
+  if (max_ctx <= 0 || hd <= 0 || (hd & 1) || !cos_out || !sin_out || !(theta > 0.f))
+    return fail("rope_tables: bad arguments");
+  const int half = hd / 2;
+  for (int p = 0; p < max_ctx; ++p)
+    for (int d = 0; d < half; ++d) {
+      const float freq = 1.f / std::pow(theta, static_cast<float>(2 * d) / static_cast<float>(hd));
+      cos_out[static_cast<size_t>(p) * half + d] = std::cos(static_cast<float>(p) * freq);
+      sin_out[static_cast<size_t>(p) * half + d] = std::sin(static_cast<float>(p) * freq);
+    }
+  return 0;
+}
+
+int cpi_hip_store_kv_device_pos(const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc,
+                                const int* pos, int kv_hidden, int max_ctx, cpi_stream_t s) {
+  if (!k || !v || !kc || !vc || !pos || kv_hidden <= 0) return fail("store_kv: bad arguments");
+  hipLaunchKernelGGL(cpi::store_kv_kernel, dim3(grid_for(kv_hidden, 256)), dim3(256), 0, S(s), k, v,
+                     kc, vc, pos, kv_hidden, max_ctx);
+  return check(hipGetLastError(), "store_kv");
+}
+
+int cpi_hip_copy_int(const int* src, int* dst, cpi_stream_t s) {
+  if (!src || !dst) return fail("copy_int: null");
+  hipLaunchKernelGGL(cpi::copy_int_kernel, dim3(1), dim3(1), 0, S(s), src, dst);
+  return check(hipGetLastError(), "copy_int");
+}
+int cpi_hip_increment_int(int* v, cpi_stream_t s) {
+  if (!v) return fail("increment_int: null");
+  hipLaunchKernelGGL(cpi::increment_int_kernel, dim3(1), dim3(1), 0, S(s), v);
+  return check(hipGetLastError(), "increment_int");
+}
+
+#define CPI_EW(name, kern, ...)                                                  \
+  if (n <= 0) return 0;                                                          \
+  hipLaunchKernelGGL(kern, dim3(grid_for(n, 256)), dim3(256), 0, S(s), __VA_ARGS__); \
+  return check(hipGetLastError(), name);
+
+int cpi_hip_add_inplace(uint16_t* x, const uint16_t* y, int n, cpi_stream_t s) {
+  if (!x || !y) return fail("add_inplace: null");
+  CPI_EW("add_inplace", cpi::add_inplace_kernel, x, y, n)
+}
+int cpi_hip_silu_mul(const uint16_t* g, const uint16_t* u, uint16_t* o, int n, cpi_stream_t s) {
+  if (!g || !u || !o) return fail("silu_mul: null");
+  CPI_EW("silu_mul", cpi::silu_mul_kernel, g, u, o, n)
+}
+int cpi_hip_scale_copy(uint16_t* d, const uint16_t* src, int n, float sc, cpi_stream_t s) {
+  if (!d || !src) return fail("scale_copy: null");
+  CPI_EW("scale_copy", cpi::scale_copy_kernel, d, src, n, sc)
+}
+int cpi_hip_scale_add_inplace(uint16_t* d, const uint16_t* src, int n, float sc, cpi_stream_t s) {
+  if (!d || !src) return fail("scale_add_inplace: null");
+  CPI_EW("scale_add_inplace", cpi::scale_add_kernel, d, src, n, sc)
+}
+
+int cpi_hip_moe_router_topk_softmax(const uint16_t* logits, int experts, int top_k, int* idx,
+                                    float* prob, cpi_stream_t s) {
+  if (!logits || !idx || !prob || experts <= 0 || experts > 64 || top_k <= 0)
+    return fail("moe_router_topk_softmax: experts must be in [1, 64], top_k > 0");
+  hipLaunchKernelGGL(cpi::router_topk_kernel, dim3(1), dim3(64), 0, S(s), logits, experts, top_k,
+                     idx, prob);
+  return check(hipGetLastError(), "moe_router_topk_softmax");
+}
+
+int cpi_hip_argmax_float(const float* x, int n, int* out, cpi_stream_t s) {
+  if (!x || !out || n <= 0) return fail("argmax_float: bad arguments");
+  hipLaunchKernelGGL(cpi::argmax_kernel, dim3(1), dim3(1024), 0, S(s), x, n, out);
+  return check(hipGetLastError(), "argmax_float");
+}
+
+int cpi_hip_quantize_rowwise_fp16_to_int8(const uint16_t* src, int8_t* dst, float* scales,
+                                          int rows, int cols, int max_q, cpi_stream_t s) {
+  if (!src || !dst || !scales || rows <= 0 || cols <= 0 || max_q <= 0 || max_q > 127)
+    return fail("quantize_rowwise: bad arguments");
+  hipLaunchKernelGGL(cpi::quantize_rowwise_kernel, dim3(rows), dim3(256), 0, S(s), src, dst,
+                     scales, cols, max_q);
+  return check(hipGetLastError(), "quantize_rowwise");
+}
+
+int cpi_hip_pack_rowwise_int8_to_int4(const int8_t* src, int8_t* dst, int rows, int cols,
+                                      cpi_stream_t s) {
+  if (!src || !dst || rows <= 0 || cols <= 0) return fail("pack_int4: bad arguments");
+  const size_t n = static_cast<size_t>(rows) * ((cols + 1) / 2);
+  hipLaunchKernelGGL(cpi::pack_int4_kernel, dim3(grid_for(n, 256)), dim3(256), 0, S(s), src, dst,
+                     rows, cols);
+  return check(hipGetLastError(), "pack_int4");
+}
+
+int cpi_hip_unpack_int4_to_int8(const int8_t* src, int8_t* dst, int rows, int cols,
+                                cpi_stream_t s) {
+  if (!src || !dst || rows <= 0 || cols <= 0) return fail("unpack_int4: bad arguments");
+  const size_t n = static_cast<size_t>(rows) * cols;
+  hipLaunchKernelGGL(cpi::unpack_int4_kernel, dim3(grid_for(n, 256)), dim3(256), 0, S(s), src,
+                     dst, rows, cols);
+  return check(hipGetLastError(), "unpack_int4");
+}
+
+int cpi_hip_dequant_rowwise_int8_to_fp16(const int8_t* src, const float* sc, uint16_t* dst,
+                                         int rows, int cols, cpi_stream_t s) {
+  if (!src || !sc || !dst || rows <= 0 || cols <= 0) return fail("dequant_rowwise: bad arguments");
+  const size_t n = static_cast<size_t>(rows) * cols;
+  hipLaunchKernelGGL(cpi::dequant_rowwise_kernel, dim3(grid_for(n, 256)), dim3(256), 0, S(s), src,
+                     sc, dst, rows, cols);
+  return check(hipGetLastError(), "dequant_rowwise");
+}
+
+int cpi_hip_attention_prefill(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int,
+                              int, int, int, int, cpi_stream_t) {
+  return fail("attention_prefill: not built yet");
+}
+
+}  // extern "C"

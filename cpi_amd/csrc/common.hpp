@@ -1,0 +1,66 @@
+// Shared device/host helpers for the gfx950 decode kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <cstdint>
+#include <cstddef>
+
+namespace cpi {
+
+typedef _Float16 f16;
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float h2f(uint16_t b) {
+  return static_cast<float>(__builtin_bit_cast(f16, b));
+}
+__device__ __forceinline__ uint16_t f2h(float v) {
+  return __builtin_bit_cast(uint16_t, static_cast<f16>(v));
+}
+__device__ __forceinline__ f16x2 as_h2(uint32_t v) {
+  return __builtin_bit_cast(f16x2, v);
+}
+__device__ __forceinline__ uint32_t h2_bits(f16 a, f16 b) {
+  f16x2 v;
+  v.x = a;
+  v.y = b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
+}
+
+// Butterfly sum over a power-of-two group of adjacent lanes.
+template <int WIDTH>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < WIDTH; m <<= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+// Block-wide sum; every thread receives the result.  `red` needs
+// blockDim.x/64 floats of shared memory.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int nw = (blockDim.x + kWave - 1) / kWave;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+}  // namespace cpi

@@ -1,0 +1,266 @@
+// Small decode-step kernels for gfx950: norm, embedding, RoPE, KV store,
+// elementwise, MoE router, argmax, quantise / pack helpers, row gather.
+//
+// Each kernel restates the semantics of the reference launch it replaces
+// (cited per kernel); vector widths and block shapes are chosen for 64-lane
+// wavefronts.
+#include "common.hpp"
+#include "../../include/cpi_hip.h"
+
+namespace cpi {
+
+// ---- RMSNorm (src/kernels/kernels.cu:36-99):
+//      y = x * rsqrt(mean(x^2) + eps) * w, fp32 statistics, one block per row.
+__global__ void __launch_bounds__(256) rmsnorm_kernel(const uint16_t* x, const uint16_t* w,
+                                                      uint16_t* y, int cols, float eps) {
+  __shared__ float red[4];
+  const size_t base = static_cast<size_t>(blockIdx.x) * cols;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < cols; i += blockDim.x) {
+    const float v = h2f(x[base + i]);
+    ss += v * v;
+  }
+  ss = block_sum(ss, red);
+  const float inv = 1.f / sqrtf(ss / static_cast<float>(cols) + eps);
+  for (int i = threadIdx.x; i < cols; i += blockDim.x)
+    y[base + i] = f2h((inv * h2f(x[base + i])) * h2f(w[i]));
+}
+
+// ---- Embedding gather (src/kernels/kernels.cu:159-191).
+template <bool F32OUT>
+__global__ void embedding_kernel(const uint16_t* emb, const int* ids, void* out, int hidden) {
+  const int t = blockIdx.x;
+  const size_t row = static_cast<size_t>(ids[t]) * hidden;
+  for (int i = threadIdx.x; i < hidden; i += blockDim.x) {
+    if (F32OUT) static_cast<float*>(out)[static_cast<size_t>(t) * hidden + i] = h2f(emb[row + i]);
+    else static_cast<uint16_t*>(out)[static_cast<size_t>(t) * hidden + i] = emb[row + i];
+  }
+}
+
+// ---- Rotate-half RoPE from fp32 tables (src/kernels/kernels.cu:230-304).
+//      grid = max(nq, nk) heads, block = head_dim/2 threads.
+__global__ void rope_kernel(uint16_t* q, uint16_t* k, int nq, int nk, int hd, int pos_host,
+                            const int* pos_dev, const float* cos_t, const float* sin_t) {
+  const int head = blockIdx.x;
+  const int d = threadIdx.x;
+  const int half = hd / 2;
+  if (d >= half) return;
+  const int pos = pos_dev ? *pos_dev : pos_host;
+  const float c = cos_t[static_cast<size_t>(pos) * half + d];
+  const float s = sin_t[static_cast<size_t>(pos) * half + d];
+  auto rot = [&](uint16_t* h) {
+    const float x0 = h2f(h[d]);
+    const float x1 = h2f(h[d + half]);
+    h[d] = f2h(x0 * c - x1 * s);
+    h[d + half] = f2h(x0 * s + x1 * c);
+  };
+  if (head < nq) rot(q + static_cast<size_t>(head) * hd);
+  if (head < nk) rot(k + static_cast<size_t>(head) * hd);
+}
+
+// ---- KV store at a device position (kernels_attention_decode.cu:813-853).
+__global__ void store_kv_kernel(const uint16_t* k, const uint16_t* v, uint16_t* kc, uint16_t* vc,
+                                const int* pos, int kv_hidden, int max_ctx) {
+  const int p = *pos;
+  if (p < 0 || p >= max_ctx) return;
+  const size_t base = static_cast<size_t>(p) * kv_hidden;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < kv_hidden; i += gridDim.x * blockDim.x) {
+    kc[base + i] = k[i];
+    vc[base + i] = v[i];
+  }
+}
+
+__global__ void copy_int_kernel(const int* src, int* dst) { *dst = *src; }
+__global__ void increment_int_kernel(int* v) { *v += 1; }
+
+// ---- elementwise fp16 ops (kernels_ops_matvec.cu:54-113)
+__global__ void add_inplace_kernel(uint16_t* x, const uint16_t* y, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    x[i] = f2h(h2f(x[i]) + h2f(y[i]));
+}
+__global__ void silu_mul_kernel(const uint16_t* g, const uint16_t* u, uint16_t* o, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+    const float gv = h2f(g[i]);
+    o[i] = f2h((gv / (1.f + expf(-gv))) * h2f(u[i]));
+  }
+}
+__global__ void scale_copy_kernel(uint16_t* dst, const uint16_t* src, int n, float s) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    dst[i] = f2h(h2f(src[i]) * s);
+}
+__global__ void scale_add_kernel(uint16_t* dst, const uint16_t* src, int n, float s) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
+    dst[i] = f2h(h2f(dst[i]) + h2f(f2h(h2f(src[i]) * s)));
+}
+
+// ---- MoE router: softmax over experts, greedy top-k with strict '>',
+//      renormalised over the picked experts (kernels_ops_matvec.cu:115-193,
+//      cpu_engine.cpp:560-606).  Single thread: experts <= 64.
+__global__ void router_topk_kernel(const uint16_t* logits, int experts, int top_k, int* idx,
+                                   float* prob) {
+  if (threadIdx.x != 0) return;
+  float pr[64];
+  float mx = h2f(logits[0]);
+  for (int e = 1; e < experts; ++e) mx = fmaxf(mx, h2f(logits[e]));
+  float sum = 0.f;
+  for (int e = 0; e < experts; ++e) {
+    pr[e] = expf(h2f(logits[e]) - mx);
+    sum += pr[e];
+  }
+  const float inv = 1.f / fmaxf(sum, 1e-8f);
+  for (int e = 0; e < experts; ++e) pr[e] *= inv;
+  unsigned long long used = 0;
+  int pick[8];
+  float pp[8];
+  const int kk = top_k < 8 ? top_k : 8;
+  float psum = 0.f;
+  for (int k = 0; k < kk; ++k) {
+    int best = -1;
+    float bp = -1.f;
+    for (int e = 0; e < experts; ++e) {
+      if (used & (1ull << e)) continue;
+      if (pr[e] > bp) { bp = pr[e]; best = e; }
+    }
+    pick[k] = best < 0 ? 0 : best;
+    pp[k] = bp > 0.f ? bp : 0.f;
+    if (best >= 0) used |= 1ull << best;
+    psum += pp[k];
+  }
+  const float ip = 1.f / fmaxf(psum, 1e-8f);
+  for (int k = 0; k < top_k; ++k) {
+    idx[k] = k < kk ? pick[k] : 0;
+    prob[k] = k < kk ? pp[k] * ip : 0.f;
+  }
+}
+
+// ---- argmax with the CPU engine's tie rule (std::max_element: lowest index
+//      among equal maxima; cpu_engine.cpp:726-729).  One block of 1024.
+__device__ __forceinline__ void argmax_merge(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+
+__device__ void block_argmax(const float* x, int n, float& bv, int& bi) {
+  __shared__ float sv[16];
+  __shared__ int si[16];
+  float v = -INFINITY;
+  int idx = 0x7fffffff;
+  for (int i = threadIdx.x; i < n; i += blockDim.x) argmax_merge(v, idx, x[i], i);
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    const float ov = __shfl_xor(v, m, kWave);
+    const int oi = __shfl_xor(idx, m, kWave);
+    argmax_merge(v, idx, ov, oi);
+  }
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  if (lane == 0) { sv[wave] = v; si[wave] = idx; }
+  __syncthreads();
+  bv = sv[0];
+  bi = si[0];
+  for (int w = 1; w < static_cast<int>(blockDim.x) / kWave; ++w) argmax_merge(bv, bi, sv[w], si[w]);
+  if (bi == 0x7fffffff) bi = 0;  // all NaN: report index 0
+}
+
+__global__ void __launch_bounds__(1024) argmax_kernel(const float* x, int n, int* out) {
+  float v;
+  int i;
+  block_argmax(x, n, v, i);
+  if (threadIdx.x == 0) *out = i;
+}
+
+// Greedy step tail used inside the captured decode graph: the argmax becomes
+// the next input token, is appended to the output ring at *step, and the
+// position/step counters advance (replaces argmax + copy_int + increment_int,
+// llama_engine_graph.cpp:472-474).
+__global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* x, int n, int* token,
+                                                              int* position, int* step,
+                                                              int* ring, int ring_len) {
+  float v;
+  int i;
+  block_argmax(x, n, v, i);
+  if (threadIdx.x == 0) {
+    *token = i;
+    const int s = *step;
+    ring[s % ring_len] = i;
+    *step = s + 1;
+    *position += 1;
+  }
+}
+
+// ---- quantise / pack / dequant (kernels_ops_matvec.cu:225-327, 449-487)
+__global__ void __launch_bounds__(256) quantize_rowwise_kernel(const uint16_t* src, int8_t* dst,
+                                                               float* scales, int cols, int max_q) {
+  __shared__ float red[4];
+  __shared__ float inv_s;
+  const size_t base = static_cast<size_t>(blockIdx.x) * cols;
+  float m = 0.f;
+  for (int i = threadIdx.x; i < cols; i += blockDim.x) m = fmaxf(m, fabsf(h2f(src[base + i])));
+  m = wave_max(m);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x / 64] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float bm = red[0];
+    for (int w = 1; w < static_cast<int>(blockDim.x) / 64; ++w) bm = fmaxf(bm, red[w]);
+    float s = bm / static_cast<float>(max_q);
+    if (s < 1e-8f) s = 1e-8f;
+    scales[blockIdx.x] = s;
+    inv_s = 1.f / s;
+  }
+  __syncthreads();
+  const float inv = inv_s;
+  for (int i = threadIdx.x; i < cols; i += blockDim.x) {
+    int q = __float2int_rn(h2f(src[base + i]) * inv);
+    q = max(-max_q, min(max_q, q));
+    dst[base + i] = static_cast<int8_t>(q);
+  }
+}
+
+__global__ void pack_int4_kernel(const int8_t* src, int8_t* dst, int rows, int cols) {
+  const int pc = (cols + 1) / 2;
+  const size_t total = static_cast<size_t>(rows) * pc;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t r = i / pc, c2 = i % pc;
+    const int8_t* row = src + r * cols;
+    const int lo = max(-8, min(7, static_cast<int>(row[2 * c2])));
+    const int hi = (2 * c2 + 1 < static_cast<size_t>(cols)) ? max(-8, min(7, static_cast<int>(row[2 * c2 + 1]))) : 0;
+    dst[i] = static_cast<int8_t>((lo & 0xF) | ((hi & 0xF) << 4));
+  }
+}
+
+__global__ void unpack_int4_kernel(const int8_t* src, int8_t* dst, int rows, int cols) {
+  const int pc = (cols + 1) / 2;
+  const size_t total = static_cast<size_t>(rows) * cols;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t r = i / cols, c = i % cols;
+    const uint32_t b = static_cast<uint8_t>(src[r * pc + c / 2]);
+    const uint32_t nib = (c & 1) ? (b >> 4) : (b & 0xF);
+    dst[i] = static_cast<int8_t>(static_cast<int>(nib ^ 8u) - 8);
+  }
+}
+
+__global__ void dequant_rowwise_kernel(const int8_t* src, const float* sc, uint16_t* dst, int rows,
+                                       int cols) {
+  const size_t total = static_cast<size_t>(rows) * cols;
+  for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+       i += static_cast<size_t>(gridDim.x) * blockDim.x)
+    dst[i] = f2h(static_cast<float>(src[i]) * sc[i / cols]);
+}
+
+// ---- row gather for fused weight layouts (16-byte granules when possible)
+__global__ void gather_rows_kernel(const uint8_t* src, uint8_t* dst, const int* idx, int rows,
+                                   size_t row_bytes) {
+  const int r = blockIdx.x;
+  if (r >= rows) return;
+  const uint8_t* s = src + static_cast<size_t>(idx[r]) * row_bytes;
+  uint8_t* d = dst + static_cast<size_t>(r) * row_bytes;
+  if ((row_bytes & 15) == 0 && (reinterpret_cast<uintptr_t>(s) & 15) == 0 &&
+      (reinterpret_cast<uintptr_t>(d) & 15) == 0) {
+    for (size_t i = threadIdx.x; i < row_bytes / 16; i += blockDim.x)
+      reinterpret_cast<uint4*>(d)[i] = reinterpret_cast<const uint4*>(s)[i];
+  } else {
+    for (size_t i = threadIdx.x; i < row_bytes; i += blockDim.x) d[i] = s[i];
+  }
+}
+
+}  // namespace cpi

@@ -1,0 +1,267 @@
+/*
+ * cpi_hip.h — C-ABI of the MI355X (gfx950) decode kernels.
+ *
+ * Every entry point is stream-ordered on the caller's hipStream_t, never
+ * allocates, never synchronises the host, and is safe to record into a HIP
+ * graph (device-position variants read the decode position from device
+ * memory).  Pointers are device pointers; "half" data is IEEE binary16 passed
+ * as uint16_t so that no HIP/CUDA type appears in the signatures.
+ *
+ * Return value: 0 on success, a positive hipError_t from the launch, or
+ * CPI_HIP_EINVAL (-1) when an argument violates a documented precondition.
+ * cpi_hip_last_error_string() describes the most recent failure on the
+ * calling thread.
+ *
+ * Each declaration cites the reference interface it replaces
+ * (kurulav1/cpi, include/runtime/kernels.cuh unless stated otherwise).
+ */
+#ifndef CPI_HIP_H
+#define CPI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* cpi_stream_t; /* a hipStream_t; NULL = the null stream */
+
+#define CPI_HIP_EINVAL (-1)
+
+/* Library / runtime helpers — replaces include/runtime/cuda_utils.cuh:12-18
+ * (CUDA_CHECK text, can_fit_on_device). */
+const char* cpi_hip_last_error_string(void);
+int cpi_hip_version(void);
+int cpi_hip_can_fit_on_device(size_t bytes, size_t safety_margin_bytes); /* 1 / 0 */
+
+/* ------------------------------------------------------------------------
+ * Weight-only GEMV family.  W is row-major [out_features, in_features].
+ *   weight formats (wfmt):
+ *     CPI_W_F16     fp16 weights, no scales
+ *     CPI_W_I8ROW   int8 [R, K] + fp32 scale per row            (.int8/.scale)
+ *     CPI_W_I4ROW   int4 packed [R, K/2] low-nibble-first,
+ *                   two's complement, + fp32 scale per row       (.int4/.scale)
+ *     CPI_W_I4G32   same packing + fp16 scale per 32-column group
+ *                   [R, K/32]                                    (.int4/.gscale)
+ *   A scale tensor holding ONE fp32 value (global scale) is accepted for the
+ *   row formats by passing scale_count = 1.
+ *   x is fp16 or fp32 (x_is_f32); accumulation is fp32.
+ *   Preconditions: in_features % 32 == 0 (I4*), % 16 (I8ROW), % 8 (F16);
+ *   weights 16-byte aligned.
+ * ---------------------------------------------------------------------- */
+enum { CPI_W_F16 = 0, CPI_W_I8ROW = 1, CPI_W_I4ROW = 2, CPI_W_I4G32 = 3 };
+
+/* y[r] = fp16(scale[r] * sum_k q[r,k] x[k])
+ * replaces launch_weight_only_int4_matvec (kernels.cuh:649-656) and, with
+ * fp16 group scales, the group-32 extension of the same call. */
+int cpi_hip_weight_only_int4_matvec(const int8_t* w_packed, const float* scales,
+                                    const uint16_t* x, uint16_t* y,
+                                    int out_features, int in_features,
+                                    cpi_stream_t stream);
+int cpi_hip_weight_only_int4g32_matvec(const int8_t* w_packed,
+                                       const uint16_t* group_scales,
+                                       const uint16_t* x, uint16_t* y,
+                                       int out_features, int in_features,
+                                       cpi_stream_t stream);
+/* replaces launch_weight_only_int8_matvec (kernels.cuh:521-527). */
+int cpi_hip_weight_only_int8_matvec(const int8_t* w, const float* scales,
+                                    const uint16_t* x, uint16_t* y,
+                                    int out_features, int in_features,
+                                    cpi_stream_t stream);
+/* replaces launch_rowmajor_half_gemv_f16 / _f32 (kernels.cuh:741-776). */
+int cpi_hip_rowmajor_half_gemv_f16(const uint16_t* w, const uint16_t* x,
+                                   uint16_t* y, int out_features,
+                                   int in_features, cpi_stream_t stream);
+int cpi_hip_rowmajor_half_gemv_f32(const uint16_t* w, const uint16_t* x,
+                                   float* y, int out_features,
+                                   int in_features, cpi_stream_t stream);
+/* Dual GEMV sharing x, fp16 outputs — replaces
+ * launch_weight_only_int4_matvec_dual_dp4a / int8 dual (kernels.cuh:629-733)
+ * with weight-only (fp16-activation) arithmetic.  w_a and w_b must use the
+ * same format; scales_* follow the format. */
+int cpi_hip_weight_only_dual_matvec(int wfmt,
+                                    const void* w_a, const void* scales_a,
+                                    const void* w_b, const void* scales_b,
+                                    const uint16_t* x, uint16_t* y_a,
+                                    uint16_t* y_b, int out_features,
+                                    int in_features, cpi_stream_t stream);
+
+/* Generic fused GEMV used by the resident engine.  Replaces the per-layer
+ * sequence rmsnorm -> quantize_rowwise -> *_matvec_dp4a -> rope ->
+ * store_kv -> add_inplace / silu_mul issued by
+ * src/engine/llama_engine_forward_decode.cpp and llama_engine_graph.cpp:166-480.
+ *
+ *   prologue: if norm_w != NULL the input is rmsnorm(x)*norm_w with eps
+ *             (kernels.cu:36-99 semantics, fp32 statistics);
+ *   epilogue: one of
+ *     CPI_EPI_STORE_F32  y_f32[r] = v
+ *     CPI_EPI_STORE_F16  y_f16[r] = fp16(v)
+ *     CPI_EPI_RESID_ADD  y_f32[r] += v            (residual stream, fp32)
+ *     CPI_EPI_SWIGLU     rows interleaved by cpi_hip_swiglu_row_order:
+ *                        y_f32[i] = silu(w1 x)[i] * (w3 x)[i]
+ *     CPI_EPI_QKV_ROPE   rows ordered by cpi_hip_qkv_row_order: q is rotated
+ *                        (rotate-half RoPE, cos/sin table [max_ctx, hd/2])
+ *                        and written to y_f32; k is rotated and v copied into
+ *                        the fp16 KV cache row *position.
+ * ---------------------------------------------------------------------- */
+enum {
+  CPI_EPI_STORE_F32 = 0,
+  CPI_EPI_STORE_F16 = 1,
+  CPI_EPI_RESID_ADD = 2,
+  CPI_EPI_SWIGLU = 3,
+  CPI_EPI_QKV_ROPE = 4
+};
+
+typedef struct cpi_gemv_desc {
+  int wfmt;               /* CPI_W_* */
+  const void* w;          /* device weights (row order per epilogue) */
+  const void* scales;     /* fp32 [R] / fp16 [R, K/32] / NULL */
+  int scale_count;        /* number of scale entries (1 = global scale) */
+  int out_features;       /* R (device rows, incl. both halves for SWIGLU) */
+  int in_features;        /* K */
+  const void* x;          /* input [K] */
+  int x_is_f32;
+  const uint16_t* norm_w; /* optional fp16 RMSNorm weight [K] */
+  float norm_eps;
+  int epilogue;           /* CPI_EPI_* */
+  void* y;                /* output (see epilogue) */
+  /* CPI_EPI_QKV_ROPE only */
+  int num_heads, num_kv_heads, head_dim;
+  const int* position;    /* device int */
+  const float* rope_cos;  /* [max_ctx, head_dim/2] */
+  const float* rope_sin;
+  uint16_t* k_cache;      /* this layer's [max_ctx, kv_dim] fp16 */
+  uint16_t* v_cache;
+  int max_context;
+} cpi_gemv_desc;
+
+int cpi_hip_gemv(const cpi_gemv_desc* d, cpi_stream_t stream);
+
+/* Host helpers for the fused row orders (no device work). out has R ints:
+ * device row i holds logical row out[i]. */
+int cpi_hip_qkv_row_order(int num_heads, int num_kv_heads, int head_dim,
+                          int* out);
+int cpi_hip_swiglu_row_order(int intermediate, int* out);
+
+/* Device row gather: dst row i = src row idx[i] (row_bytes each); idx is a
+ * device int array.  Used once at load time to lay out fused weights. */
+int cpi_hip_gather_rows(const void* src, void* dst, const int* idx, int rows,
+                        size_t row_bytes, cpi_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Decode attention (exact online softmax, split-K over context, GQA).
+ * q fp32 or fp16 [num_heads*head_dim] (q_is_f32), caches fp16
+ * [max_ctx, num_kv_heads*head_dim], out fp32 or fp16 [num_heads*head_dim].
+ * Scratch: fp32 [num_heads * CPI_ATTN_MAX_SPLITS * (head_dim + 2)].
+ * Replaces launch_attention_step / _device_pos (kernels.cuh:216-275):
+ * chunk_stats + chunk_reduce, gqa_decode_kernel and the tiled kernel.
+ * ---------------------------------------------------------------------- */
+#define CPI_ATTN_MAX_SPLITS 256
+size_t cpi_hip_attention_scratch_floats(int num_heads, int head_dim);
+
+int cpi_hip_attention_decode(const void* q, int q_is_f32,
+                             const uint16_t* k_cache, const uint16_t* v_cache,
+                             void* out, int out_is_f32,
+                             int seq_len,         /* host length, or <=0 ... */
+                             const int* position, /* ... then seq = *position+1 */
+                             int num_heads, int num_kv_heads, int head_dim,
+                             int max_context, int sliding_window,
+                             float* scratch, cpi_stream_t stream);
+/* Reference-shaped wrappers (fp16 in/out). */
+int cpi_hip_attention_step(const uint16_t* q, const uint16_t* k_cache,
+                           const uint16_t* v_cache, uint16_t* out,
+                           int seq_len, int num_heads, int num_kv_heads,
+                           int head_dim, float* scratch, cpi_stream_t stream);
+int cpi_hip_attention_step_device_pos(const uint16_t* q,
+                                      const uint16_t* k_cache,
+                                      const uint16_t* v_cache, uint16_t* out,
+                                      const int* position, int num_heads,
+                                      int num_kv_heads, int head_dim,
+                                      int max_context, float* scratch,
+                                      cpi_stream_t stream);
+
+/* Causal prefill attention for a chunk whose K/V are already in the cache —
+ * replaces launch_attention_prefill (kernels.cuh:316-325).  q/out fp16
+ * [num_tokens, num_heads*head_dim]. */
+int cpi_hip_attention_prefill(const uint16_t* q, const uint16_t* k_cache,
+                              const uint16_t* v_cache, uint16_t* out,
+                              int num_tokens, int start_position,
+                              int num_heads, int num_kv_heads, int head_dim,
+                              cpi_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Small ops.
+ * ---------------------------------------------------------------------- */
+/* launch_rmsnorm (kernels.cuh:46-52) */
+int cpi_hip_rmsnorm(const uint16_t* x, const uint16_t* weight, uint16_t* y,
+                    int rows, int cols, float eps, cpi_stream_t stream);
+/* launch_embedding_lookup (kernels.cuh:82-87) */
+int cpi_hip_embedding_lookup(const uint16_t* embedding, const int* token_ids,
+                             uint16_t* out, int num_tokens, int hidden,
+                             cpi_stream_t stream);
+/* Embedding row -> fp32 residual stream (engine path). */
+int cpi_hip_embedding_lookup_f32(const uint16_t* embedding,
+                                 const int* token_ids, float* out,
+                                 int num_tokens, int hidden,
+                                 cpi_stream_t stream);
+/* launch_rope_inplace_table / _device_pos (kernels.cuh:128-156) */
+int cpi_hip_rope_inplace_table(uint16_t* q, uint16_t* k, int num_heads_q,
+                               int num_heads_k, int head_dim, int position,
+                               const float* cos_table, const float* sin_table,
+                               cpi_stream_t stream);
+int cpi_hip_rope_inplace_device_pos(uint16_t* q, uint16_t* k, int num_heads_q,
+                                    int num_heads_k, int head_dim,
+                                    const int* position,
+                                    const float* cos_table,
+                                    const float* sin_table,
+                                    cpi_stream_t stream);
+/* Host construction of the fp32 RoPE tables, same formula as the reference
+ * (llama_engine_lifecycle.cpp:270-296, cpu_engine.cpp:1033-1045). */
+int cpi_rope_tables(int max_context, int head_dim, float theta, float* cos_out,
+                    float* sin_out);
+/* launch_store_kv_device_pos (kernels.cuh:277-284) */
+int cpi_hip_store_kv_device_pos(const uint16_t* k, const uint16_t* v,
+                                uint16_t* k_cache, uint16_t* v_cache,
+                                const int* position, int kv_hidden,
+                                int max_context, cpi_stream_t stream);
+/* launch_copy_int / launch_increment_int (kernels.cuh:293-294) */
+int cpi_hip_copy_int(const int* src, int* dst, cpi_stream_t stream);
+int cpi_hip_increment_int(int* value, cpi_stream_t stream);
+/* launch_add_inplace (kernels.cuh:339), launch_silu_mul (:379-383) */
+int cpi_hip_add_inplace(uint16_t* x, const uint16_t* y, int n,
+                        cpi_stream_t stream);
+int cpi_hip_silu_mul(const uint16_t* gate, const uint16_t* up, uint16_t* out,
+                     int n, cpi_stream_t stream);
+/* launch_scale_copy / launch_scale_add_inplace (kernels.cuh:396-417) */
+int cpi_hip_scale_copy(uint16_t* dst, const uint16_t* src, int n, float scale,
+                       cpi_stream_t stream);
+int cpi_hip_scale_add_inplace(uint16_t* dst, const uint16_t* src, int n,
+                              float scale, cpi_stream_t stream);
+/* launch_moe_router_topk_softmax (kernels.cuh:431-436) */
+int cpi_hip_moe_router_topk_softmax(const uint16_t* logits, int experts,
+                                    int top_k, int* topk_idx, float* topk_prob,
+                                    cpi_stream_t stream);
+/* launch_argmax_float (kernels.cuh:785-788): lowest index among maxima. */
+int cpi_hip_argmax_float(const float* logits, int n, int* out_index,
+                         cpi_stream_t stream);
+/* launch_quantize_rowwise_fp16_to_int8 (kernels.cuh:490-496) */
+int cpi_hip_quantize_rowwise_fp16_to_int8(const uint16_t* src, int8_t* dst,
+                                          float* scales, int rows, int cols,
+                                          int max_q, cpi_stream_t stream);
+/* launch_pack_rowwise_int8_to_int4 (kernels.cuh:502-506) */
+int cpi_hip_pack_rowwise_int8_to_int4(const int8_t* src, int8_t* dst,
+                                      int rows, int cols, cpi_stream_t stream);
+/* launch_dequant_rowwise_int8_to_fp16 (kernels.cuh:467-472) */
+int cpi_hip_dequant_rowwise_int8_to_fp16(const int8_t* src, const float* scales,
+                                         uint16_t* dst, int rows, int cols,
+                                         cpi_stream_t stream);
+/* Unpack packed int4 to int8 (bit-exact nibble decode, test hook for
+ * kernels_weight_only_matvec.cu:35-43). */
+int cpi_hip_unpack_int4_to_int8(const int8_t* src, int8_t* dst, int rows,
+                                int cols, cpi_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CPI_HIP_H */

@@ -1,0 +1,303 @@
+"""GPU parity of the HIP kernels against the CPU oracle, called through the
+C-ABI (libcpi_hip.so).  Tolerances are stated per test."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from cpi_amd import _lib, ll2c
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    from tests import gpu_util as G
+
+FMTS = {"f16": _lib.W_F16, "i8": _lib.W_I8ROW, "i4": _lib.W_I4ROW, "i4g32": _lib.W_I4G32}
+
+
+def make_weights(fmt, R, K, seed, random_lowbit=False):
+    """Returns (blob uint8, scales array or None, dequantised fp32 [R,K])."""
+    rng = np.random.default_rng(seed)
+    if fmt == "i4g32" and random_lowbit:
+        blob = rng.integers(0, 256, R * K // 2, dtype=np.uint8)
+        sc = np.abs(rng.standard_normal(R * K // 32).astype(np.float32) * 0.01).astype(np.float16)
+    else:
+        w = (rng.standard_normal((R, K)) * 0.05).astype(np.float16)
+        if fmt == "f16":
+            blob, sc = w.view(np.uint8).reshape(-1), None
+        elif fmt == "i8":
+            q, sc = ll2c.quantize_int8_rowwise(w)
+            blob = q.view(np.uint8).reshape(-1)
+        elif fmt == "i4":
+            blob, sc = ll2c.quantize_int4_rowwise(w)
+        else:
+            blob, sc = ll2c.quantize_int4_g32(w)
+        blob = blob.reshape(-1)
+    deq = ll2c.dequant(fmt, blob, None if sc is None else sc.reshape(-1).view(np.uint8), R, K)
+    return blob, (None if sc is None else sc.reshape(-1)), deq
+
+
+def tol(fmt, deq, x):
+    """Per-row bound: fp16 rounding of x (int formats) contributes at most
+    2^-11 relative per product; fp16 weights use a hi/lo split of x."""
+    c = 2e-3 if fmt != "f16" else 2e-5
+    return c * np.sqrt(((deq * x[None, :]) ** 2).sum(1)) + 1e-6
+
+
+@pytest.mark.parametrize("fmt", ["f16", "i8", "i4", "i4g32"])
+@pytest.mark.parametrize("R,K", [(40, 96 // 32 * 32), (8, 32), (300, 544), (12288, 4096), (22016, 4096),
+                                 (4096, 11008), (4096, 4096)])
+def test_gemv_parity(fmt, R, K):
+    print(f"[gemv] fmt={fmt} R={R} K={K}", flush=True)
+    blob, sc, deq = make_weights(fmt, R, K, R + K, random_lowbit=(R >= 4096))
+    x = np.random.default_rng(K).standard_normal(K).astype(np.float32)
+    ref = oracle.gemv(fmt, blob, sc, R, K, x)
+    w, s = G.dev(blob), (G.dev(sc) if sc is not None else None)
+    y = G.empty(R * 4)
+    G.gemv(FMTS[fmt], w, s, (sc.size if sc is not None else 0), R, K, G.dev(x), y)
+    got = G.host(y, np.float32, R)
+    bound = tol(fmt, deq, x)
+    assert (np.abs(got - ref) <= bound).all(), np.abs(got - ref).max()
+
+
+@pytest.mark.parametrize("fmt", ["i8", "i4", "i4g32"])
+def test_gemv_unpack_bit_exact(fmt):
+    """A one-hot x makes the GEMV return column k of the dequantised matrix:
+    q * scale computed exactly, so the result must match bit for bit."""
+    R, K = 64, 128
+    blob, sc, deq = make_weights(fmt, R, K, 11)
+    w, s = G.dev(blob), G.dev(sc)
+    for k in (0, 1, 7, 8, 31, 32, 63, 127):
+        x = np.zeros(K, np.float32)
+        x[k] = 1.0
+        y = G.empty(R * 4)
+        G.gemv(FMTS[fmt], w, s, sc.size, R, K, G.dev(x), y)
+        got = G.host(y, np.float32, R)
+        assert (got.view(np.uint32) == deq[:, k].astype(np.float32).view(np.uint32)).all(), k
+
+
+def test_unpack_int4_exhaustive():
+    src = np.arange(256, dtype=np.uint8)
+    out = G.empty(512)
+    _lib.call("cpi_hip_unpack_int4_to_int8", G.ptr(G.dev(src)), G.ptr(out), 1, 512, G.stream())
+    got = G.host(out, np.int8, 512)
+    exp = np.array([oracle.lib().oracle_int4_nibble(b, h) for b in range(256) for h in (0, 1)], np.int8)
+    assert (got == exp).all()
+
+
+def test_reference_shaped_wrappers():
+    R, K = 256, 512
+    x = np.random.default_rng(1).standard_normal(K).astype(np.float16)
+    xf = x.astype(np.float32)
+    for fmt, fn in (("i4", "cpi_hip_weight_only_int4_matvec"), ("i8", "cpi_hip_weight_only_int8_matvec"),
+                    ("i4g32", "cpi_hip_weight_only_int4g32_matvec")):
+        blob, sc, deq = make_weights(fmt, R, K, 5)
+        y = G.empty(R * 2)
+        _lib.call(fn, G.ptr(G.dev(blob)), G.ptr(G.dev(sc)), G.ptr(G.dev(x)), G.ptr(y), R, K, G.stream())
+        got = G.host(y, np.float16, R).astype(np.float32)
+        ref = oracle.gemv(fmt, blob, sc, R, K, xf)
+        assert np.abs(got - ref).max() <= 2e-3 * np.abs(ref).max() + 1e-3
+    blob, _, deq = make_weights("f16", R, K, 6)
+    y = G.empty(R * 4)
+    _lib.call("cpi_hip_rowmajor_half_gemv_f32", G.ptr(G.dev(blob)), G.ptr(G.dev(x)), G.ptr(y), R, K, G.stream())
+    np.testing.assert_allclose(G.host(y, np.float32, R), oracle.gemv("f16", blob, None, R, K, xf), atol=1e-4)
+
+
+def test_gemv_rejects_bad_shapes():
+    w = G.empty(1024)
+    y = G.empty(1024)
+    x = G.empty(1024)
+    with pytest.raises(_lib.CpiHipError):
+        G.gemv(_lib.W_I4ROW, w, w, 4, 4, 40, x, y)  # K % 32 != 0
+
+
+@pytest.mark.parametrize("fmt", ["f16", "i4g32"])
+def test_gemv_norm_and_residual(fmt):
+    R, K = 512, 1024
+    rng = np.random.default_rng(4)
+    blob, sc, deq = make_weights(fmt, R, K, 9)
+    x = rng.standard_normal(K).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float16)
+    resid = rng.standard_normal(R).astype(np.float32)
+    xn = oracle.rmsnorm(x, nw, 1e-5)
+    ref = resid + oracle.gemv(fmt, blob, sc, R, K, xn)
+    y = G.dev(resid)
+    G.gemv(FMTS[fmt], G.dev(blob), G.dev(sc) if sc is not None else None, sc.size if sc is not None else 0,
+           R, K, G.dev(x), y, epilogue=_lib.EPI_RESID_ADD, norm_w=G.dev(nw), eps=1e-5)
+    got = G.host(y, np.float32, R)
+    assert (np.abs(got - ref) <= tol(fmt, deq, xn) + 1e-5).all()
+
+
+@pytest.mark.parametrize("fmt", ["f16", "i4g32"])
+def test_gemv_swiglu(fmt):
+    I, K = 352, 512
+    blob, sc, deq = make_weights(fmt, 2 * I, K, 12)
+    x = np.random.default_rng(2).standard_normal(K).astype(np.float32)
+    order = np.zeros(2 * I, np.int32)
+    _lib.call("cpi_hip_swiglu_row_order", I, order.ctypes.data_as(ctypes.POINTER(ctypes.c_int)))
+    rows = _split_rows(blob, sc, fmt, 2 * I, K)
+    wperm = np.ascontiguousarray(rows[0][order])
+    sperm = None if rows[1] is None else np.ascontiguousarray(rows[1][order])
+    y = G.empty(I * 4)
+    G.gemv(FMTS[fmt], G.dev(wperm), None if sperm is None else G.dev(sperm),
+           0 if sperm is None else sperm.size, 2 * I, K, G.dev(x), y, epilogue=_lib.EPI_SWIGLU)
+    h = oracle.gemv(fmt, blob, sc, 2 * I, K, x)
+    ref = np.array([oracle.lib().oracle_silu(float(g)) for g in h[:I]], np.float32) * h[I:]
+    got = G.host(y, np.float32, I)
+    np.testing.assert_allclose(got, ref, atol=(2e-3 if fmt != "f16" else 1e-5) * np.abs(ref).max() + 1e-5)
+
+
+def _split_rows(blob, sc, fmt, R, K):
+    bpr = {"f16": 2 * K, "i8": K, "i4": K // 2, "i4g32": K // 2}[fmt]
+    w = blob.reshape(R, bpr)
+    if sc is None:
+        return w, None
+    return w, (sc.reshape(R, -1) if fmt == "i4g32" else sc.reshape(R, 1))
+
+
+@pytest.mark.parametrize("fmt", ["f16", "i4g32", "i8"])
+@pytest.mark.parametrize("nh,nkv,hd", [(32, 4, 64), (8, 8, 128), (8, 2, 128)])
+def test_gemv_qkv_rope_kvstore(fmt, nh, nkv, hd):
+    H = 512 if fmt != "i8" else 256
+    R = (nh + 2 * nkv) * hd
+    max_ctx, pos, theta = 64, 37, 10000.0
+    rng = np.random.default_rng(nh + hd)
+    blob, sc, deq = make_weights(fmt, R, H, 21)
+    x = rng.standard_normal(H).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
+    order = np.zeros(R, np.int32)
+    _lib.call("cpi_hip_qkv_row_order", nh, nkv, hd, order.ctypes.data_as(ctypes.POINTER(ctypes.c_int)))
+    assert sorted(order) == list(range(R))
+    w, s = _split_rows(blob, sc, fmt, R, H)
+    wperm = np.ascontiguousarray(w[order])
+    sperm = None if s is None else np.ascontiguousarray(s[order])
+    cos_t, sin_t = oracle.rope_tables(max_ctx, hd, theta)
+    kc = G.empty(max_ctx * nkv * hd * 2)
+    vc = G.empty(max_ctx * nkv * hd * 2)
+    q = G.empty(nh * hd * 4)
+    posd = G.dev(np.array([pos], np.int32))
+    G.gemv(FMTS[fmt], G.dev(wperm), None if sperm is None else G.dev(sperm),
+           0 if sperm is None else sperm.size, R, H, G.dev(x), q, epilogue=_lib.EPI_QKV_ROPE,
+           norm_w=G.dev(nw), eps=1e-5, num_heads=nh, num_kv_heads=nkv, head_dim=hd, position=posd,
+           rope_cos=G.dev(cos_t), rope_sin=G.dev(sin_t), k_cache=kc, v_cache=vc, max_context=max_ctx)
+    xn = oracle.rmsnorm(x, nw, 1e-5)
+    full = oracle.gemv(fmt, blob, sc, R, H, xn)
+    qr, kr = oracle.rope(full[:nh * hd], full[nh * hd:(nh + nkv) * hd], pos, nh, nkv, hd, cos_t, sin_t)
+    vr = full[(nh + nkv) * hd:]
+    a = (2e-3 if fmt != "f16" else 2e-5) * np.abs(full).max() * 4 + 1e-5
+    np.testing.assert_allclose(G.host(q, np.float32, nh * hd), qr, atol=a)
+    kch = G.host(kc, np.float16).reshape(max_ctx, -1)
+    vch = G.host(vc, np.float16).reshape(max_ctx, -1)
+    np.testing.assert_allclose(kch[pos].astype(np.float32), kr, atol=a + 2e-3 * np.abs(kr).max())
+    np.testing.assert_allclose(vch[pos].astype(np.float32), vr, atol=a + 2e-3 * np.abs(vr).max())
+    assert not np.any(np.delete(kch, pos, 0)) and not np.any(np.delete(vch, pos, 0))
+
+
+@pytest.mark.parametrize("nh,nkv,hd,seq", [(32, 8, 128, 1), (32, 8, 128, 512), (32, 8, 128, 4096),
+                                           (32, 4, 64, 200), (32, 32, 128, 640), (32, 8, 128, 32768),
+                                           (8, 8, 64, 63), (16, 8, 128, 65)])
+def test_attention_parity(nh, nkv, hd, seq):
+    print(f"[attn] nh={nh} nkv={nkv} hd={hd} seq={seq}", flush=True)
+    rng = np.random.default_rng(seq)
+    max_ctx = seq + 3
+    kv = nkv * hd
+    kc = rng.standard_normal((max_ctx, kv)).astype(np.float16)
+    vc = rng.standard_normal((max_ctx, kv)).astype(np.float16)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    ref = oracle.attention(q, kc[:seq].astype(np.float32), vc[:seq].astype(np.float32), seq, nh, nkv, hd)
+    scratch = G.empty(_lib.lib().cpi_hip_attention_scratch_floats(nh, hd) * 4)
+    out = G.empty(nh * hd * 4)
+    kd, vd = G.dev(kc), G.dev(vc)
+    _lib.call("cpi_hip_attention_decode", G.ptr(G.dev(q)), 1, G.ptr(kd), G.ptr(vd), G.ptr(out), 1, seq, None,
+              nh, nkv, hd, max_ctx, 0, G.ptr(scratch), G.stream())
+    np.testing.assert_allclose(G.host(out, np.float32, nh * hd), ref, atol=2e-4)
+    # device-position variant, fp16 in/out
+    out16 = G.empty(nh * hd * 2)
+    pos = G.dev(np.array([seq - 1], np.int32))
+    q16 = G.dev(q.astype(np.float16))
+    _lib.call("cpi_hip_attention_step_device_pos", G.ptr(q16), G.ptr(kd), G.ptr(vd), G.ptr(out16), G.ptr(pos),
+              nh, nkv, hd, max_ctx, G.ptr(scratch), G.stream())
+    ref16 = oracle.attention(q.astype(np.float16).astype(np.float32), kc[:seq].astype(np.float32),
+                             vc[:seq].astype(np.float32), seq, nh, nkv, hd)
+    np.testing.assert_allclose(G.host(out16, np.float16, nh * hd).astype(np.float32), ref16, atol=2e-3)
+
+
+def test_attention_sliding_window():
+    nh, nkv, hd, seq, win = 8, 2, 64, 300, 77
+    rng = np.random.default_rng(5)
+    kc = rng.standard_normal((seq, nkv * hd)).astype(np.float16)
+    vc = rng.standard_normal((seq, nkv * hd)).astype(np.float16)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    ref = oracle.attention(q, kc.astype(np.float32), vc.astype(np.float32), seq, nh, nkv, hd, win)
+    scratch = G.empty(_lib.lib().cpi_hip_attention_scratch_floats(nh, hd) * 4)
+    out = G.empty(nh * hd * 4)
+    _lib.call("cpi_hip_attention_decode", G.ptr(G.dev(q)), 1, G.ptr(G.dev(kc)), G.ptr(G.dev(vc)), G.ptr(out), 1,
+              seq, None, nh, nkv, hd, seq, win, G.ptr(scratch), G.stream())
+    np.testing.assert_allclose(G.host(out, np.float32, nh * hd), ref, atol=2e-4)
+
+
+def test_small_ops():
+    rng = np.random.default_rng(8)
+    s = G.stream()
+    # rmsnorm (fp16 in/out)
+    x = rng.standard_normal((3, 200)).astype(np.float16)
+    w = (1 + 0.1 * rng.standard_normal(200)).astype(np.float16)
+    y = G.empty(x.nbytes)
+    _lib.call("cpi_hip_rmsnorm", G.ptr(G.dev(x)), G.ptr(G.dev(w)), G.ptr(y), 3, 200, 1e-5, s)
+    got = G.host(y, np.float16).reshape(3, 200).astype(np.float32)
+    for r in range(3):
+        np.testing.assert_allclose(got[r], oracle.rmsnorm(x[r].astype(np.float32), w, 1e-5), atol=4e-3)
+    # argmax with ties -> lowest index
+    lg = rng.standard_normal(32000).astype(np.float32)
+    lg[[100, 20000]] = 9.0
+    o = G.empty(16)
+    _lib.call("cpi_hip_argmax_float", G.ptr(G.dev(lg)), 32000, G.ptr(o), s)
+    assert G.host(o, np.int32)[0] == 100 == oracle.argmax(lg)
+    # router KAT (src/tests/moe_kernel_parity_test.cu:80-132)
+    logits = np.array([1.2, -0.7, 3.5, 2.1, -1.0, 0.4], np.float16)
+    idx, pr = G.empty(8), G.empty(8)
+    _lib.call("cpi_hip_moe_router_topk_softmax", G.ptr(G.dev(logits)), 6, 2, G.ptr(idx), G.ptr(pr), s)
+    ridx, rpr = oracle.router_topk(logits.astype(np.float32), 2)
+    assert list(G.host(idx, np.int32, 2)) == [2, 3] == list(ridx)
+    np.testing.assert_allclose(G.host(pr, np.float32, 2), rpr, atol=5e-3)
+    # scale_copy / scale_add KAT form (moe_kernel_parity_test.cu:134-192)
+    n = 64
+    i = np.arange(n)
+    a = (0.35 * np.sin(0.13 * i)).astype(np.float16)
+    b = (0.65 * np.cos(0.09 * i)).astype(np.float16)
+    d = G.empty(n * 2)
+    _lib.call("cpi_hip_scale_copy", G.ptr(d), G.ptr(G.dev(a)), n, 0.5, s)
+    _lib.call("cpi_hip_scale_add_inplace", G.ptr(d), G.ptr(G.dev(b)), n, 0.25, s)
+    np.testing.assert_allclose(G.host(d, np.float16).astype(np.float32),
+                               a.astype(np.float32) * 0.5 + b.astype(np.float32) * 0.25, atol=2e-3)
+    # embedding
+    emb = rng.standard_normal((50, 64)).astype(np.float16)
+    ids = np.array([3, 49, 0], np.int32)
+    out = G.empty(3 * 64 * 4)
+    _lib.call("cpi_hip_embedding_lookup_f32", G.ptr(G.dev(emb)), G.ptr(G.dev(ids)), G.ptr(out), 3, 64, s)
+    np.testing.assert_array_equal(G.host(out, np.float32).reshape(3, 64), emb[ids].astype(np.float32))
+    # rope (fp16 in place) vs oracle
+    hd, nq, nk = 64, 4, 2
+    cos_t, sin_t = oracle.rope_tables(16, hd, 10000.0)
+    qh = rng.standard_normal(nq * hd).astype(np.float16)
+    kh = rng.standard_normal(nk * hd).astype(np.float16)
+    qd, kd = G.dev(qh), G.dev(kh)
+    _lib.call("cpi_hip_rope_inplace_table", G.ptr(qd), G.ptr(kd), nq, nk, hd, 9, G.ptr(G.dev(cos_t)),
+              G.ptr(G.dev(sin_t)), s)
+    qr, kr = oracle.rope(qh.astype(np.float32), kh.astype(np.float32), 9, nq, nk, hd, cos_t, sin_t)
+    np.testing.assert_allclose(G.host(qd, np.float16).astype(np.float32), qr, atol=4e-3)
+    np.testing.assert_allclose(G.host(kd, np.float16).astype(np.float32), kr, atol=4e-3)
+    # quantize rowwise + pack -> unpack round trip
+    m = rng.standard_normal((4, 64)).astype(np.float16)
+    q8, sc = G.empty(256), G.empty(16)
+    _lib.call("cpi_hip_quantize_rowwise_fp16_to_int8", G.ptr(G.dev(m)), G.ptr(q8), G.ptr(sc), 4, 64, 7, s)
+    pk = G.empty(128)
+    _lib.call("cpi_hip_pack_rowwise_int8_to_int4", G.ptr(q8), G.ptr(pk), 4, 64, s)
+    un = G.empty(256)
+    _lib.call("cpi_hip_unpack_int4_to_int8", G.ptr(pk), G.ptr(un), 4, 64, s)
+    qv = G.host(q8, np.int8, 256)
+    assert (G.host(un, np.int8, 256) == qv).all() and np.abs(qv).max() <= 7
+    scv = G.host(sc, np.float32, 4)
+    np.testing.assert_allclose(scv, np.abs(m.astype(np.float32)).max(1) / 7, rtol=1e-6)

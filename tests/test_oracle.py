@@ -1,0 +1,165 @@
+"""Pins the CPU oracle (oracle/oracle.c) against closed forms, brute force,
+the reference's own known-answer test and an independent float64 decoder.
+Runs on the CPU only."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from cpi_amd import ll2c
+from tests.numpy_ref import RefModel
+
+
+def test_fp16_conversion_exhaustive():
+    bits = np.arange(1 << 16, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([oracle.lib().oracle_fp16_to_fp32(int(b)) for b in bits], np.float32)
+    same = (got.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(got) & np.isnan(ref))
+    assert same.all()
+
+
+def test_int4_nibble_exhaustive():
+    # closed form: sign-extend the 4-bit two's complement value (low nibble first)
+    for b in range(256):
+        lo = ((b & 0xF) ^ 8) - 8
+        hi = ((b >> 4) ^ 8) - 8
+        assert oracle.lib().oracle_int4_nibble(b, 0) == lo
+        assert oracle.lib().oracle_int4_nibble(b, 1) == hi
+    packed = np.arange(256, dtype=np.uint8).reshape(1, 256)
+    q = ll2c.unpack_int4(packed, 512)
+    assert (ll2c.pack_int4(q) == packed).all()
+
+
+@pytest.mark.parametrize("fmt", ["f16", "i8", "i4", "i4g32"])
+@pytest.mark.parametrize("R,K", [(37, 96), (64, 256), (5, 1000 // 32 * 32)])
+def test_gemv_vs_float64(fmt, R, K):
+    rng = np.random.default_rng(R * 1000 + K)
+    w = (rng.standard_normal((R, K)) * 0.05).astype(np.float16)
+    x = rng.standard_normal(K).astype(np.float32)
+    if fmt == "f16":
+        blob, sc = w.view(np.uint8), None
+    elif fmt == "i8":
+        q, sc = ll2c.quantize_int8_rowwise(w)
+        blob = q.view(np.uint8)
+    elif fmt == "i4":
+        blob, sc = ll2c.quantize_int4_rowwise(w)
+    else:
+        blob, sc = ll2c.quantize_int4_g32(w)
+    deq = ll2c.dequant(fmt, blob.reshape(-1), None if sc is None else sc.reshape(-1).view(np.uint8), R, K)
+    ref = deq.astype(np.float64) @ x.astype(np.float64)
+    y = oracle.gemv(fmt, blob, sc, R, K, x)
+    np.testing.assert_allclose(y, ref, rtol=0, atol=1e-5 * np.abs(deq).sum(1).max() * np.abs(x).max() + 1e-6)
+
+
+def test_gemv_single_global_scale():
+    rng = np.random.default_rng(3)
+    q = rng.integers(-127, 128, (8, 64)).astype(np.int8)
+    s = np.array([0.125], np.float32)
+    x = rng.standard_normal(64).astype(np.float32)
+    y = oracle.gemv("i8", q, s, 8, 64, x)
+    np.testing.assert_allclose(y, (q.astype(np.float64) * 0.125) @ x, atol=1e-4)
+
+
+def test_quantizers_closed_form():
+    w = np.array([[0.7, -0.3, 0.1, 0.0, -0.7, 0.04, 0.2, -0.1]], np.float16)
+    q, s = ll2c.quantize_int4_rowwise(w)
+    assert np.isclose(s[0], np.float32(np.float16(0.7)) / 7)
+    assert list(ll2c.unpack_int4(q, 8)[0]) == [7, -3, 1, 0, -7, 0, 2, -1]
+    assert q[0, 0] == ((7 & 0xF) | ((-3 & 0xF) << 4))
+    q8, s8 = ll2c.quantize_int8_rowwise(w)
+    assert q8[0, 0] == 127 and q8[0, 4] == -127
+    z, sz = ll2c.quantize_int8_rowwise(np.zeros((1, 4), np.float16))
+    assert sz[0] == np.float32(1e-8) and (z == 0).all()
+    # round-trip bound |w - q s| <= s / 2 for in-range values
+    rng = np.random.default_rng(0)
+    m = rng.standard_normal((16, 64)).astype(np.float16)
+    pk, gs = ll2c.quantize_int4_g32(m)
+    d = ll2c.dequant("i4g32", pk.reshape(-1), gs.reshape(-1).view(np.uint8), 16, 64)
+    bound = np.repeat(gs.astype(np.float32), 32, axis=1) / 2 + 1e-3
+    assert (np.abs(d - m.astype(np.float32)) <= bound).all()
+
+
+def test_rmsnorm_closed_form():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(333).astype(np.float32)
+    w = (1 + 0.1 * rng.standard_normal(333)).astype(np.float16)
+    ref = x / np.sqrt(np.mean(x.astype(np.float64) ** 2) + 1e-5) * w.astype(np.float64)
+    np.testing.assert_allclose(oracle.rmsnorm(x, w, 1e-5), ref, rtol=2e-6, atol=2e-6)
+
+
+@pytest.mark.parametrize("theta", [10000.0, 500000.0])
+def test_rope_is_complex_rotation(theta):
+    hd, nh, nkv = 64, 4, 2
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    k = rng.standard_normal(nkv * hd).astype(np.float32)
+    c, s = oracle.rope_tables(300, hd, theta)
+    for pos in (0, 1, 17, 299):
+        q2, k2 = oracle.rope(q, k, pos, nh, nkv, hd, c, s)
+        for src, dst, heads in ((q, q2, nh), (k, k2, nkv)):
+            x = src.reshape(heads, hd).astype(np.float64)
+            ang = pos * theta ** (-2.0 * np.arange(hd // 2) / hd)
+            z = (x[:, :32] + 1j * x[:, 32:]) * np.exp(1j * ang)
+            ref = np.concatenate([z.real, z.imag], 1).reshape(-1)
+            np.testing.assert_allclose(dst, ref, atol=3e-4 if pos > 100 else 2e-5)
+        # norm preserved per (d, d+half) pair
+        np.testing.assert_allclose(np.linalg.norm(q2), np.linalg.norm(q), rtol=1e-5)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,seq,window", [(8, 2, 32, 1, 0), (8, 8, 16, 50, 0), (4, 1, 64, 77, 20)])
+def test_attention_vs_softmax(nh, nkv, hd, seq, window):
+    from scipy.special import softmax
+    rng = np.random.default_rng(seq)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    kc = rng.standard_normal((seq, nkv * hd)).astype(np.float32)
+    vc = rng.standard_normal((seq, nkv * hd)).astype(np.float32)
+    out = oracle.attention(q, kc, vc, seq, nh, nkv, hd, window)
+    g = nh // nkv
+    lo = seq - window if window and seq > window else 0
+    for h in range(nh):
+        K = kc[lo:, (h // g) * hd:(h // g + 1) * hd].astype(np.float64)
+        V = vc[lo:, (h // g) * hd:(h // g + 1) * hd].astype(np.float64)
+        p = softmax(K @ q[h * hd:(h + 1) * hd] / np.sqrt(hd))
+        np.testing.assert_allclose(out[h * hd:(h + 1) * hd], p @ V, atol=2e-5)
+
+
+def test_router_reference_kat():
+    # src/tests/moe_kernel_parity_test.cu:80-132: logits {1.2,-0.7,3.5,2.1,-1.0,0.4}, top-2 -> {2,3}
+    logits = np.array([1.2, -0.7, 3.5, 2.1, -1.0, 0.4], np.float16).astype(np.float32)
+    idx, prob = oracle.router_topk(logits, 2)
+    assert list(idx) == [2, 3]
+    e = np.exp(np.float64(logits[2]) - logits[3])
+    np.testing.assert_allclose(prob, [e / (1 + e), 1 / (1 + e)], atol=1e-6)
+    assert abs(prob.sum() - 1) < 1e-6
+
+
+def test_argmax_first_max():
+    x = np.array([1, 5, 3, 5, -1], np.float32)
+    assert oracle.argmax(x) == 1
+
+
+TINY = dict(vocab_size=512, hidden_size=128, intermediate_size=256, num_layers=2, num_heads=4,
+            num_kv_heads=2, max_seq_len=64, rope_theta=10000.0, norm_eps=1e-5)
+
+
+@pytest.mark.parametrize("attn,mlp,extra", [
+    ("f16", "f16", {}),
+    ("f16", "i8", {}),
+    ("f16", "i4", {}),
+    ("i4g32", "i4g32", {}),
+    ("f16", "f16", {"num_local_experts": 4, "num_experts_per_tok": 2, "expert_intermediate_size": 96}),
+    ("f16", "f16", {"sliding_window": 6, "rope_theta": 500000.0}),
+])
+def test_engine_vs_float64_decoder(tmp_path, attn, mlp, extra):
+    cfg = ll2c.Config(**{**TINY, **extra})
+    path = str(tmp_path / "m.ll2c")
+    ll2c.write_synthetic(path, ll2c.SynthSpec(cfg, attn_fmt=attn, mlp_fmt=mlp, seed=7, std=0.05, norm_jitter=0.1))
+    prompt = np.random.default_rng(0).integers(0, cfg.vocab_size, 9)
+    eng = oracle.Engine(path, 64)
+    ids, lg = eng.generate(prompt, 12, eos=-1, logit_steps=12)
+    ref = RefModel(path)
+    rids, rlg = ref.generate(prompt, 12)
+    scale = np.abs(rlg).max()
+    np.testing.assert_allclose(lg, rlg, atol=2e-5 * max(scale, 1))
+    assert (ids == rids).all()
