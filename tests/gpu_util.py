@@ -23,19 +23,26 @@ def empty(nbytes: int) -> torch.Tensor:
     return torch.zeros(max(nbytes, 16), dtype=torch.uint8, device="cuda")
 
 
+_keep = []  # tensors whose raw pointers were handed out; freed at the next sync
+
+
 def host(t: torch.Tensor, dtype, n=None) -> np.ndarray:
     torch.cuda.synchronize()
+    _keep.clear()
     a = t.cpu().numpy().view(dtype)
     return a if n is None else a[:n]
 
 
 def ptr(t) -> ctypes.c_void_p:
+    if t is not None:
+        _keep.append(t)
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
 
 
 def gemv(fmt: int, w, scales, scale_count, R, K, x, y, epilogue=_lib.EPI_STORE_F32, x_f32=True,
          norm_w=None, eps=1e-5, **kw):
     d = _lib.GemvDesc()
+    _keep.extend(t for t in (w, scales, x, y, norm_w, *kw.values()) if isinstance(t, torch.Tensor))
     d.wfmt, d.w, d.scales, d.scale_count = fmt, w.data_ptr(), (scales.data_ptr() if scales is not None else 0), scale_count
     d.out_features, d.in_features = R, K
     d.x, d.x_is_f32 = x.data_ptr(), int(x_f32)
