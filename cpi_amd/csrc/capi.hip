@@ -45,7 +45,8 @@ int gemv_common(int wfmt, int epi, const void* w, const void* scales, int scale_
   if (ce == 0) return fail(std::string(who) + ": unknown weight format");
   if (K % ce != 0)
     return fail(std::string(who) + ": in_features must be a multiple of " + std::to_string(ce));
-  if ((reinterpret_cast<uintptr_t>(w) & 15) != 0) return fail(std::string(who) + ": weights not 16-byte aligned");
+  if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15) != 0)
+    return fail(std::string(who) + ": weights and x must be 16-byte aligned");
   if (wfmt != CPI_W_F16 && !scales) return fail(std::string(who) + ": missing scales");
   cpi::GemvParams p{};
   p.w = w;
@@ -118,7 +119,9 @@ int cpi_hip_gemv(const cpi_gemv_desc* d, cpi_stream_t s) {
     return fail("gemv: null pointer or empty shape");
   if (d->in_features % ce != 0)
     return fail("gemv: in_features must be a multiple of " + std::to_string(ce));
-  if ((reinterpret_cast<uintptr_t>(d->w) & 15) != 0) return fail("gemv: weights not 16-byte aligned");
+  if (((reinterpret_cast<uintptr_t>(d->w) | reinterpret_cast<uintptr_t>(d->x) |
+        reinterpret_cast<uintptr_t>(d->norm_w)) & 15) != 0)
+    return fail("gemv: weights, x and norm_w must be 16-byte aligned");
   if (d->wfmt != CPI_W_F16 && !d->scales) return fail("gemv: missing scales");
   if (d->wfmt == CPI_W_I8ROW || d->wfmt == CPI_W_I4ROW) {
     if (d->scale_count != 1 && d->scale_count != d->out_features)

@@ -23,6 +23,8 @@
 //    product keeps ~22 bits of the activation.
 //  * Optional RMSNorm prologue (statistics in fp32) and fused epilogues
 //    (residual add, SwiGLU, RoPE + KV-cache store) remove the small launches.
+#include <cstdlib>
+
 #include "common.hpp"
 #include "../../include/cpi_hip.h"
 
@@ -32,7 +34,7 @@ constexpr int kChunkCols = 8;                 // 16-byte chunks per row per step
 constexpr int kTileRows = kWave / kChunkCols; // rows per wave tile
 constexpr int kWavesPerBlock = 4;
 constexpr int kBlock = kWave * kWavesPerBlock;
-constexpr int kUnroll = 4;
+constexpr int kUnroll = 8;
 
 template <int FMT> struct FmtT;
 template <> struct FmtT<CPI_W_F16> {
@@ -146,18 +148,20 @@ __device__ __forceinline__ float chunk_dot(const u32x4 w, const uint32_t* p, flo
     }
     return acc;
   } else if constexpr (FMT == CPI_W_I8ROW) {
+    // (w ^ 0x80808080) & 0x00FF00FF | 0x64006400 == (w & 0x00FF00FF) ^ 0x64806480
     const uint4 a = *reinterpret_cast<const uint4*>(p);
     const uint4 b = *reinterpret_cast<const uint4*>(p + 4);
     const uint32_t pp[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    float t = __builtin_bit_cast(float, p[8]);
+    float t0 = __builtin_bit_cast(float, p[8]), t1 = 0.f;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      const uint32_t u = wd[d] ^ 0x80808080u;
-      t = dot2((u & 0x00FF00FFu) | 0x64006400u, pp[2 * d], t);
-      t = dot2(((u >> 8) & 0x00FF00FFu) | 0x64006400u, pp[2 * d + 1], t);
+      t0 = dot2((wd[d] & 0x00FF00FFu) ^ 0x64806480u, pp[2 * d], t0);
+      t1 = dot2(((wd[d] >> 8) & 0x00FF00FFu) ^ 0x64806480u, pp[2 * d + 1], t1);
     }
-    return acc + t;
+    return acc + (t0 + t1);
   } else {
+    // Two's complement nibble n -> offset binary n ^ 8, placed under the
+    // exponent of 1024.0:  (w & M) ^ (0x6400 | 8<<shift) per half.
     uint32_t pp[16];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -167,17 +171,38 @@ __device__ __forceinline__ float chunk_dot(const u32x4 w, const uint32_t* p, flo
       pp[4 * i + 2] = a.z;
       pp[4 * i + 3] = a.w;
     }
-    float t = __builtin_bit_cast(float, p[16]);
+    float t0 = __builtin_bit_cast(float, p[16]), t1 = 0.f;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      const uint32_t u = wd[d] ^ 0x88888888u;
+      const uint32_t u = wd[d];
       const uint32_t u8 = u >> 8;
-      t = dot2((u & 0x000F000Fu) | 0x64006400u, pp[4 * d + 0], t);
-      t = dot2((u & 0x00F000F0u) | 0x64006400u, pp[4 * d + 1], t);
-      t = dot2((u8 & 0x000F000Fu) | 0x64006400u, pp[4 * d + 2], t);
-      t = dot2((u8 & 0x00F000F0u) | 0x64006400u, pp[4 * d + 3], t);
+      t0 = dot2((u & 0x000F000Fu) ^ 0x64086408u, pp[4 * d + 0], t0);
+      t1 = dot2((u & 0x00F000F0u) ^ 0x64806480u, pp[4 * d + 1], t1);
+      t0 = dot2((u8 & 0x000F000Fu) ^ 0x64086408u, pp[4 * d + 2], t0);
+      t1 = dot2((u8 & 0x00F000F0u) ^ 0x64806480u, pp[4 * d + 3], t1);
     }
-    return t;  // caller applies the group scale / accumulates
+    return t0 + t1;  // caller applies the group scale / accumulates
+  }
+}
+
+// Eight consecutive activations starting at 8*c (16- or 32-byte aligned).
+template <bool XF32>
+__device__ __forceinline__ void load_x8(const void* x, int c, float* v) {
+  if constexpr (XF32) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4* q = reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + 8 * c);
+    const f32x4 a = q[0], b = q[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  } else {
+    const u32x4 a = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(x) + 8 * c);
+    const uint32_t d[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f16x2 h = as_h2(d[q]);
+      v[2 * q] = static_cast<float>(h.x);
+      v[2 * q + 1] = static_cast<float>(h.y);
+    }
   }
 }
 
@@ -188,24 +213,188 @@ __device__ __forceinline__ float load_x(const void* x, int i) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel.
+// Kernel pieces.
+// ---------------------------------------------------------------------------
+struct TileCtx {
+  const uint8_t* wrow;   // this lane's weight row
+  const uint16_t* grow;  // this lane's group-scale row (I4G32)
+  int row;
+  bool row_ok;
+};
+
+template <int FMT>
+__device__ __forceinline__ TileCtx tile_ctx(const GemvParams& p, int t, int r, int nchunks,
+                                            size_t row_bytes) {
+  TileCtx c;
+  c.row = t * kTileRows + r;
+  c.row_ok = c.row < p.R;
+  const int rowc = c.row_ok ? c.row : (p.R - 1);
+  c.wrow = static_cast<const uint8_t*>(p.w) + static_cast<size_t>(rowc) * row_bytes;
+  c.grow = nullptr;
+  if constexpr (FMT == CPI_W_I4G32)
+    c.grow = static_cast<const uint16_t*>(p.scales) + static_cast<size_t>(rowc) * nchunks;
+  return c;
+}
+
+// Issue the weight (and group-scale) loads of batch b of a tile.
+template <int FMT>
+__device__ __forceinline__ void load_batch(const TileCtx& tc, int b, int j, int nchunks,
+                                           u32x4 (&w)[kUnroll], float (&g)[kUnroll]) {
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int c = (b * kUnroll + u) * kChunkCols + j;
+    const int cc = c < nchunks ? c : nchunks - 1;  // clamped: always a valid address
+    w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tc.wrow) + cc);
+    if constexpr (FMT == CPI_W_I4G32) g[u] = h2f(tc.grow[cc]);
+  }
+}
+
+template <int FMT>
+__device__ __forceinline__ float compute_batch(const uint32_t* lds, int b, int j, int nchunks,
+                                               const u32x4 (&w)[kUnroll], const float (&g)[kUnroll],
+                                               float acc) {
+  using F = FmtT<FMT>;
+  if ((b * kUnroll + kUnroll) * kChunkCols <= nchunks) {  // full batch: no predication
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int c = (b * kUnroll + u) * kChunkCols + j;
+      const uint32_t* pc = lds + c * F::kStride;
+      if constexpr (FMT == CPI_W_I4G32) acc = fmaf(g[u], chunk_dot<FMT>(w[u], pc, 0.f), acc);
+      else if constexpr (FMT == CPI_W_I4ROW) acc += chunk_dot<FMT>(w[u], pc, 0.f);
+      else acc = chunk_dot<FMT>(w[u], pc, acc);
+    }
+    return acc;
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const int c = (b * kUnroll + u) * kChunkCols + j;
+    if (c < nchunks) {
+      const uint32_t* pc = lds + c * F::kStride;
+      if constexpr (FMT == CPI_W_I4G32) acc = fmaf(g[u], chunk_dot<FMT>(w[u], pc, 0.f), acc);
+      else if constexpr (FMT == CPI_W_I4ROW) acc += chunk_dot<FMT>(w[u], pc, 0.f);
+      else acc = chunk_dot<FMT>(w[u], pc, acc);
+    }
+  }
+  return acc;
+}
+
+// Reduce the 8 chunk-column partials of each row and run the epilogue.
+template <int FMT, int EPI>
+__device__ __forceinline__ void finish_tile(const GemvParams& p, int t, int r, int j, const TileCtx& tc,
+                                            float acc) {
+  acc = group_sum<kChunkCols>(acc);
+  const int row = tc.row;
+  const bool row_ok = tc.row_ok;
+  if constexpr (FMT == CPI_W_I8ROW || FMT == CPI_W_I4ROW) {
+    const float* sc = static_cast<const float*>(p.scales);
+    acc *= (p.scale_count == 1) ? sc[0] : sc[row_ok ? row : p.R - 1];
+  }
+  if constexpr (EPI == CPI_EPI_STORE_F32) {
+    if (j == 0 && row_ok) static_cast<float*>(p.y)[row] = acc;
+  } else if constexpr (EPI == CPI_EPI_STORE_F16) {
+    if (j == 0 && row_ok) static_cast<uint16_t*>(p.y)[row] = f2h(acc);
+  } else if constexpr (EPI == EPI_DUAL_F16) {
+    if (j == 0 && row_ok) {
+      if (row < p.rows_a) static_cast<uint16_t*>(p.y)[row] = f2h(acc);
+      else static_cast<uint16_t*>(p.y2)[row - p.rows_a] = f2h(acc);
+    }
+  } else if constexpr (EPI == CPI_EPI_RESID_ADD) {
+    if (j == 0 && row_ok) static_cast<float*>(p.y)[row] += acc;
+  } else if constexpr (EPI == CPI_EPI_SWIGLU) {
+    // tile t rows: [w1 4t..4t+3 | w3 4t..4t+3]; partner lane = lane ^ 32.
+    const float other = __shfl_xor(acc, 32, kWave);
+    if (j == 0 && r < 4) {
+      const float g = acc;
+      static_cast<float*>(p.y)[t * 4 + r] = (g / (1.f + expf(-g))) * other;
+    }
+  } else if constexpr (EPI == CPI_EPI_QKV_ROPE) {
+    const float other = __shfl_xor(acc, 32, kWave);
+    const int hd = p.hd;
+    const int half = hd >> 1;
+    const int tiles_per_head = hd / kTileRows;
+    const int q_tiles = p.nh * tiles_per_head;
+    const int k_tiles = p.nkv * tiles_per_head;
+    const int kvdim = p.nkv * hd;
+    const int pos = *p.position;
+    if (j == 0) {
+      if (t < q_tiles + k_tiles) {
+        const bool is_q = t < q_tiles;
+        const int u = is_q ? t : t - q_tiles;
+        const int head = u / tiles_per_head;
+        const int bb = u % tiles_per_head;
+        const int dd = 4 * bb + (r & 3);
+        const float c = p.rope_cos[static_cast<size_t>(pos) * half + dd];
+        const float s = p.rope_sin[static_cast<size_t>(pos) * half + dd];
+        float outv;
+        int d;
+        if (r < 4) {  // acc = x0, other = x1
+          outv = acc * c - other * s;
+          d = dd;
+        } else {      // acc = x1, other = x0
+          outv = other * s + acc * c;
+          d = dd + half;
+        }
+        if (is_q) {
+          static_cast<float*>(p.y)[head * hd + d] = outv;
+        } else if (pos < p.max_ctx) {
+          p.k_cache[static_cast<size_t>(pos) * kvdim + head * hd + d] = f2h(outv);
+        }
+      } else {
+        const int vr = (t - q_tiles - k_tiles) * kTileRows + r;
+        if (pos < p.max_ctx && vr < kvdim) p.v_cache[static_cast<size_t>(pos) * kvdim + vr] = f2h(acc);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel.  A workgroup's 4 waves cover TPW = 4/KS tiles per iteration, each
+// tile split into KS K-segments (one wave each, equal batch counts, reduced
+// through LDS in a fixed order).  Each wave walks its work as a flat sequence
+// of load batches with two register buffers: the loads of batch i+1 are in
+// flight while batch i is computed, and the first batch is issued before the
+// activation prologue so HBM latency overlaps the preparation.
 // ---------------------------------------------------------------------------
 template <int FMT, int EPI, bool XF32>
-__global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p) {
+__global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int ks) {
   using F = FmtT<FMT>;
   extern __shared__ __align__(16) uint32_t lds[];
   __shared__ float red[kWavesPerBlock];
+  __shared__ float part[kWavesPerBlock][kTileRows];
 
   const int K = p.K;
   const int nchunks = K / F::kElems;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int r = lane / kChunkCols;
+  const int j = lane % kChunkCols;
+  const int tpw = kWavesPerBlock / ks;      // tiles per workgroup iteration
+  const int seg = wave % ks;
+  const int tiles = (p.R + kTileRows - 1) / kTileRows;
+  const int steps = (nchunks + kChunkCols - 1) / kChunkCols;
+  const int nbt = (steps + kUnroll - 1) / kUnroll;  // batches per tile
+  const int nbs = (nbt + ks - 1) / ks;               // batches per segment
+  const int b0 = seg * nbs;
+  const size_t row_bytes = static_cast<size_t>(K) * 16 / F::kElems;
+  const int groups = (tiles + tpw - 1) / tpw;
+
+  int gi = blockIdx.x;                       // tile-group index of this workgroup
+  int t = gi * tpw + wave / ks;
+  int b = 0;                                 // batch index within the segment
+  TileCtx tc = tile_ctx<FMT>(p, t < tiles ? t : 0, r, nchunks, row_bytes);
+  u32x4 wa[kUnroll], wb[kUnroll];
+  float ga[kUnroll], gb[kUnroll];
+  if (gi < groups && t < tiles) load_batch<FMT>(tc, b0, j, nchunks, wa, ga);
 
   // ---- prologue: optional RMSNorm statistics, then activation preparation
   float inv_rms = 1.f;
   if (p.norm_w != nullptr) {
     float ss = 0.f;
-    for (int i = threadIdx.x; i < K; i += kBlock) {
-      const float v = load_x<XF32>(p.x, i);
-      ss += v * v;
+    for (int c = threadIdx.x; c < K / 8; c += kBlock) {
+      float v[8];
+      load_x8<XF32>(p.x, c, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
     }
     ss = block_sum(ss, red);
     inv_rms = 1.f / sqrtf(ss / static_cast<float>(K) + p.eps);
@@ -213,126 +402,63 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p) {
   for (int c = threadIdx.x; c < nchunks; c += kBlock) {
     float v[F::kElems];
 #pragma unroll
-    for (int e = 0; e < F::kElems; ++e) {
-      const int i = c * F::kElems + e;
-      float xv = load_x<XF32>(p.x, i);
-      if (p.norm_w != nullptr) xv = (inv_rms * xv) * h2f(p.norm_w[i]);
-      v[e] = xv;
+    for (int e8 = 0; e8 < F::kElems / 8; ++e8) {
+      load_x8<XF32>(p.x, c * (F::kElems / 8) + e8, v + 8 * e8);
+      if (p.norm_w != nullptr) {
+        const u32x4 nw = *reinterpret_cast<const u32x4*>(p.norm_w + (c * (F::kElems / 8) + e8) * 8);
+        const uint32_t nd[4] = {nw.x, nw.y, nw.z, nw.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const f16x2 h = as_h2(nd[q]);
+          v[8 * e8 + 2 * q] = (inv_rms * v[8 * e8 + 2 * q]) * static_cast<float>(h.x);
+          v[8 * e8 + 2 * q + 1] = (inv_rms * v[8 * e8 + 2 * q + 1]) * static_cast<float>(h.y);
+        }
+      }
     }
     prep_chunk<FMT>(v, lds + c * F::kStride);
   }
   __syncthreads();
 
-  // ---- main loop: one wave per 8-row tile, grid-stride over tiles
-  const int lane = threadIdx.x & (kWave - 1);
-  const int r = lane / kChunkCols;
-  const int j = lane % kChunkCols;
-  const int waves_total = gridDim.x * kWavesPerBlock;
-  const int tiles = (p.R + kTileRows - 1) / kTileRows;
-  const int steps = (nchunks + kChunkCols - 1) / kChunkCols;
-  const size_t row_bytes = static_cast<size_t>(K) * 16 / F::kElems;
-
-  for (int t = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave; t < tiles; t += waves_total) {
-    const int row = t * kTileRows + r;
-    const bool row_ok = row < p.R;
-    const int rowc = row_ok ? row : (p.R - 1);
-    const uint8_t* wrow = static_cast<const uint8_t*>(p.w) + static_cast<size_t>(rowc) * row_bytes;
-    const uint16_t* grow = nullptr;
-    if constexpr (FMT == CPI_W_I4G32)
-      grow = static_cast<const uint16_t*>(p.scales) + static_cast<size_t>(rowc) * nchunks;
-
-    float acc = 0.f;
-    for (int s0 = 0; s0 < steps; s0 += kUnroll) {
-      u32x4 wv[kUnroll];
-      float gs[kUnroll];
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int c = (s0 + u) * kChunkCols + j;
-        if (c < nchunks) {
-          wv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow) + c);
-          if constexpr (FMT == CPI_W_I4G32) gs[u] = h2f(grow[c]);
-        }
-      }
-#pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        const int c = (s0 + u) * kChunkCols + j;
-        if (c < nchunks) {
-          const uint32_t* pc = lds + c * F::kStride;
-          if constexpr (FMT == CPI_W_I4G32) {
-            acc = fmaf(gs[u], chunk_dot<FMT>(wv[u], pc, 0.f), acc);
-          } else if constexpr (FMT == CPI_W_I4ROW) {
-            acc += chunk_dot<FMT>(wv[u], pc, 0.f);
-          } else {
-            acc = chunk_dot<FMT>(wv[u], pc, acc);
-          }
-        }
-      }
-    }
-    acc = group_sum<kChunkCols>(acc);
-    if constexpr (FMT == CPI_W_I8ROW || FMT == CPI_W_I4ROW) {
-      const float* sc = static_cast<const float*>(p.scales);
-      acc *= (p.scale_count == 1) ? sc[0] : sc[rowc];
-    }
-
-    // ---- epilogues (value of row r lives in lane r*8)
-    if constexpr (EPI == CPI_EPI_STORE_F32) {
-      if (j == 0 && row_ok) static_cast<float*>(p.y)[row] = acc;
-    } else if constexpr (EPI == CPI_EPI_STORE_F16) {
-      if (j == 0 && row_ok) static_cast<uint16_t*>(p.y)[row] = f2h(acc);
-    } else if constexpr (EPI == EPI_DUAL_F16) {
-      if (j == 0 && row_ok) {
-        if (row < p.rows_a) static_cast<uint16_t*>(p.y)[row] = f2h(acc);
-        else static_cast<uint16_t*>(p.y2)[row - p.rows_a] = f2h(acc);
-      }
-    } else if constexpr (EPI == CPI_EPI_RESID_ADD) {
-      if (j == 0 && row_ok) static_cast<float*>(p.y)[row] += acc;
-    } else if constexpr (EPI == CPI_EPI_SWIGLU) {
-      // tile t rows: [w1 4t..4t+3 | w3 4t..4t+3]; partner lane = lane ^ 32.
-      const float other = __shfl_xor(acc, 32, kWave);
-      if (j == 0 && r < 4) {
-        const float g = acc;
-        static_cast<float*>(p.y)[t * 4 + r] = (g / (1.f + expf(-g))) * other;
-      }
-    } else if constexpr (EPI == CPI_EPI_QKV_ROPE) {
-      const float other = __shfl_xor(acc, 32, kWave);
-      const int hd = p.hd;
-      const int half = hd >> 1;
-      const int tiles_per_head = hd / kTileRows;
-      const int q_tiles = p.nh * tiles_per_head;
-      const int k_tiles = p.nkv * tiles_per_head;
-      const int kvdim = p.nkv * hd;
-      const int pos = *p.position;
-      if (j == 0) {
-        if (t < q_tiles + k_tiles) {
-          const bool is_q = t < q_tiles;
-          const int u = is_q ? t : t - q_tiles;
-          const int head = u / tiles_per_head;
-          const int b = u % tiles_per_head;
-          const int dd = 4 * b + (r & 3);
-          const float c = p.rope_cos[static_cast<size_t>(pos) * half + dd];
-          const float s = p.rope_sin[static_cast<size_t>(pos) * half + dd];
-          float outv;
-          int d;
-          if (r < 4) {  // acc = x0, other = x1
-            outv = acc * c - other * s;
-            d = dd;
-          } else {      // acc = x1, other = x0
-            outv = other * s + acc * c;
-            d = dd + half;
-          }
-          if (is_q) {
-            static_cast<float*>(p.y)[head * hd + d] = outv;
-          } else if (pos < p.max_ctx) {
-            p.k_cache[static_cast<size_t>(pos) * kvdim + head * hd + d] = f2h(outv);
-          }
-        } else {
-          const int vr = (t - q_tiles - k_tiles) * kTileRows + r;
-          if (pos < p.max_ctx && vr < kvdim)
-            p.v_cache[static_cast<size_t>(pos) * kvdim + vr] = f2h(acc);
-        }
-      }
-    }
+  float acc = 0.f;
+  // One pipeline step: prefetch the successor batch into (WN, GN) while the
+  // current batch in (WC, GC) is consumed.
+#define CPI_GEMV_STEP(WC, GC, WN, GN)                                                          \
+  {                                                                                            \
+    int gn = gi, bn = b + 1;                                                                   \
+    if (bn == nbs) { bn = 0; gn += gridDim.x; }                                                \
+    const int tn = gn * tpw + wave / ks;                                                       \
+    const TileCtx tcn = (bn == 0) ? tile_ctx<FMT>(p, tn < tiles ? tn : 0, r, nchunks, row_bytes) \
+                                  : tc;                                                        \
+    const bool tile_ok = t < tiles;                                                            \
+    if (gn < groups && tn < tiles) load_batch<FMT>(tcn, b0 + bn, j, nchunks, WN, GN);          \
+    if (tile_ok) acc = compute_batch<FMT>(lds, b0 + b, j, nchunks, WC, GC, acc);               \
+    if (b == nbs - 1) {                                                                        \
+      if (ks == 1) {                                                                           \
+        if (tile_ok) finish_tile<FMT, EPI>(p, t, r, j, tc, acc);                               \
+      } else {                                                                                 \
+        const float v = group_sum<kChunkCols>(acc);                                            \
+        if (j == 0) part[wave][r] = v;                                                         \
+        __syncthreads();                                                                       \
+        if (seg == 0 && tile_ok) {                                                             \
+          float tot = 0.f;                                                                     \
+          if (j == 0) {                                                                        \
+            tot = part[wave][r];                                                               \
+            for (int s2 = 1; s2 < ks; ++s2) tot += part[wave + s2][r];                         \
+          }                                                                                    \
+          finish_tile<FMT, EPI>(p, t, r, j, tc, tot);                                          \
+        }                                                                                      \
+        __syncthreads();                                                                       \
+      }                                                                                        \
+      acc = 0.f;                                                                               \
+    }                                                                                          \
+    gi = gn; b = bn; t = tn; tc = tcn;                                                         \
   }
+  while (gi < groups) {  // uniform across the workgroup
+    CPI_GEMV_STEP(wa, ga, wb, gb)
+    if (gi >= groups) break;
+    CPI_GEMV_STEP(wb, gb, wa, ga)
+  }
+#undef CPI_GEMV_STEP
 }
 
 // ---------------------------------------------------------------------------
@@ -340,7 +466,8 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p) {
 // ---------------------------------------------------------------------------
 namespace {
 
-int g_max_blocks = 1024;
+int g_max_blocks = 4096;
+int g_force_ks = 0;
 
 template <int FMT>
 size_t lds_bytes(int K) {
@@ -350,10 +477,19 @@ size_t lds_bytes(int K) {
 template <int FMT, int EPI, bool XF32>
 hipError_t launch(const GemvParams& p, hipStream_t s) {
   const int tiles = (p.R + kTileRows - 1) / kTileRows;
-  int blocks = (tiles + kWavesPerBlock - 1) / kWavesPerBlock;
+  // K-split so that the launch has >= ~2048 waves (8 per CU) when possible.
+  const int steps = (p.K / FmtT<FMT>::kElems + kChunkCols - 1) / kChunkCols;
+  const int nbt = (steps + kUnroll - 1) / kUnroll;
+  int ks = 1;
+  if (g_force_ks > 0) ks = g_force_ks;
+  else if (tiles < 1024 && nbt >= 4) ks = 4;
+  else if (tiles < 2048 && nbt >= 2) ks = 2;
+  if (ks > nbt) ks = nbt >= 4 ? 4 : (nbt >= 2 ? 2 : 1);
+  const int tpw = kWavesPerBlock / ks;
+  int blocks = (tiles + tpw - 1) / tpw;
   if (blocks > g_max_blocks) blocks = g_max_blocks;
   const size_t lds = lds_bytes<FMT>(p.K);
-  hipLaunchKernelGGL((gemv_kernel<FMT, EPI, XF32>), dim3(blocks), dim3(kBlock), lds, s, p);
+  hipLaunchKernelGGL((gemv_kernel<FMT, EPI, XF32>), dim3(blocks), dim3(kBlock), lds, s, p, ks);
   return hipGetLastError();
 }
 
@@ -377,7 +513,16 @@ hipError_t dispatch_x(int epi, bool xf32, const GemvParams& p, hipStream_t s) {
 
 }  // namespace
 
+void gemv_set_max_blocks(int n) { g_max_blocks = n > 0 ? n : 4096; }
+void gemv_set_ksplit(int n) { g_force_ks = (n == 1 || n == 2 || n == 4) ? n : 0; }
+
 hipError_t gemv_launch(int wfmt, int epi, bool xf32, const GemvParams& p, hipStream_t s) {
+  static const bool env_once = [] {
+    if (const char* v = getenv("CPI_GEMV_KSPLIT")) gemv_set_ksplit(atoi(v));
+    if (const char* v = getenv("CPI_GEMV_MAX_BLOCKS")) gemv_set_max_blocks(atoi(v));
+    return true;
+  }();
+  (void)env_once;
   switch (wfmt) {
     case CPI_W_F16: return dispatch_x<CPI_W_F16>(epi, xf32, p, s);
     case CPI_W_I8ROW: return dispatch_x<CPI_W_I8ROW>(epi, xf32, p, s);
@@ -397,6 +542,5 @@ int gemv_elems_per_chunk(int wfmt) {
   return 0;
 }
 
-void gemv_set_max_blocks(int n) { g_max_blocks = n > 0 ? n : 1024; }
 
 }  // namespace cpi

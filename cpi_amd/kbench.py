@@ -1,0 +1,147 @@
+"""Kernel-only GEMV / attention timing on the GPU (BASELINE configs 2 and 3).
+
+Weights rotate over >= 1 GiB of distinct copies so the 256 MB Infinity Cache
+cannot serve them; launches are captured in a HIP graph (torch.cuda.graph on
+torch's current stream, which is where the C-ABI launches go) and the replay is
+timed with HIP events on that same stream.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import torch
+
+from cpi_amd import _lib
+
+# (name, R, K): Llama-2-7B projection shapes
+GEMV_SHAPES = [("qkv", 12288, 4096), ("w13", 22016, 4096), ("w2", 4096, 11008), ("o_proj", 4096, 4096)]
+
+FMT_CODE = {"f16": _lib.W_F16, "i8": _lib.W_I8ROW, "i4": _lib.W_I4ROW, "i4g32": _lib.W_I4G32}
+
+
+def gemv_bytes(fmt: str, R: int, K: int) -> int:
+    """Algorithmic HBM bytes of one launch: weights + scales + x (fp16) + y (fp16)."""
+    if fmt == "i4g32":
+        w = R * K // 2 + R * (K // 32) * 2
+    elif fmt == "i4":
+        w = R * K // 2 + 4 * R
+    elif fmt == "i8":
+        w = R * K + 4 * R
+    else:
+        w = 2 * R * K
+    return w + 2 * K + 2 * R
+
+
+def _weights(fmt, R, K, gen):
+    if fmt in ("i4", "i4g32"):
+        w = torch.randint(0, 256, (R * K // 2,), dtype=torch.uint8, device="cuda", generator=gen)
+    elif fmt == "i8":
+        w = torch.randint(0, 256, (R * K,), dtype=torch.uint8, device="cuda", generator=gen)
+    else:
+        w = (torch.randn(R * K, device="cuda", generator=gen) * 0.02).half().view(torch.uint8)
+    if fmt == "i4g32":
+        s = (torch.randn(R * K // 32, device="cuda", generator=gen).abs() * 0.01).half()
+        sc = s.numel()
+    elif fmt in ("i4", "i8"):
+        s = torch.rand(R, device="cuda", generator=gen) * 0.01
+        sc = R
+    else:
+        s, sc = None, 0
+    return w, s, sc
+
+
+def time_gemv(fmt: str, R: int, K: int, rotate_bytes: int = 3 << 30, iters: int = 200):
+    """Returns dict(us=avg per launch, gbps=algorithmic GB/s)."""
+    gen = torch.Generator(device="cuda").manual_seed(R + K)
+    nbytes = gemv_bytes(fmt, R, K)
+    copies = max(2, int(np.ceil(rotate_bytes / nbytes)))
+    bufs = [_weights(fmt, R, K, gen) for _ in range(copies)]
+    x = torch.randn(K, device="cuda", generator=gen).half()
+    y = torch.empty(R, device="cuda", dtype=torch.float16)
+    descs = []
+    for w, s, sc in bufs:
+        d = _lib.GemvDesc()
+        d.wfmt, d.w, d.scales, d.scale_count = FMT_CODE[fmt], w.data_ptr(), (s.data_ptr() if s is not None else 0), sc
+        d.out_features, d.in_features, d.x, d.x_is_f32 = R, K, x.data_ptr(), 0
+        d.epilogue, d.y = _lib.EPI_STORE_F16, y.data_ptr()
+        descs.append(d)
+    fn = _lib.lib().cpi_hip_gemv
+
+    def launch_all(n):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for i in range(n):
+            rc = fn(ctypes.byref(descs[i % copies]), st)
+            if rc:
+                raise _lib.CpiHipError(_lib.lib().cpi_hip_last_error_string().decode())
+
+    launch_all(copies)  # warm up
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch_all(iters)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 3
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * iters)
+    del g, bufs
+    torch.cuda.empty_cache()
+    return {"fmt": fmt, "R": R, "K": K, "us": us, "bytes": nbytes, "gbps": nbytes / us / 1e3}
+
+
+def time_attention(nh, nkv, hd, ctx, iters=100, rotate_bytes=2 << 30):
+    gen = torch.Generator(device="cuda").manual_seed(ctx)
+    kvb = ctx * nkv * hd * 2 * 2
+    copies = max(2, int(np.ceil(rotate_bytes / kvb)))
+    caches = [(torch.randn(ctx * nkv * hd, device="cuda", generator=gen).half(),
+               torch.randn(ctx * nkv * hd, device="cuda", generator=gen).half()) for _ in range(copies)]
+    q = torch.randn(nh * hd, device="cuda", generator=gen)
+    out = torch.empty(nh * hd, device="cuda")
+    scratch = torch.empty(_lib.lib().cpi_hip_attention_scratch_floats(nh, hd), device="cuda")
+    fn = _lib.lib().cpi_hip_attention_decode
+
+    def launch_all(n):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for i in range(n):
+            k, v = caches[i % copies]
+            rc = fn(q.data_ptr(), 1, k.data_ptr(), v.data_ptr(), out.data_ptr(), 1, ctx, None, nh, nkv, hd,
+                    ctx, 0, scratch.data_ptr(), st)
+            if rc:
+                raise _lib.CpiHipError(_lib.lib().cpi_hip_last_error_string().decode())
+
+    launch_all(copies)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch_all(iters)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / iters
+    nbytes = 2 * ctx * nkv * hd * 2 + nh * hd * 4 * 2
+    del g, caches
+    torch.cuda.empty_cache()
+    return {"ctx": ctx, "us": us, "bytes": nbytes, "gbps": nbytes / us / 1e3}
+
+
+if __name__ == "__main__":
+    import json
+    import sys
+    fmts = sys.argv[1:] or ["i4g32", "i4", "i8", "f16"]
+    for f in fmts:
+        for name, R, K in GEMV_SHAPES:
+            r = time_gemv(f, R, K)
+            r["shape"] = name
+            print(json.dumps(r), flush=True)
+    for ctx in (512, 4096, 32768):
+        print(json.dumps(time_attention(32, 8, 128, ctx)), flush=True)
