@@ -343,6 +343,22 @@ int cpi_hip_argmax_float(const float* x, int n, int* out, cpi_stream_t s) {
   return check(hipGetLastError(), "argmax_float");
 }
 
+int cpi_hip_greedy_advance(const float* logits, int n, int* token, int* position, int* step,
+                           int* ring, int ring_len, cpi_stream_t s) {
+  if (!logits || n <= 0 || !token || !position || !step || !ring || ring_len <= 0)
+    return fail("greedy_advance: bad arguments");
+  hipLaunchKernelGGL(cpi::argmax_advance_kernel, dim3(1), dim3(1024), 0, S(s), logits, n, token,
+                     position, step, ring, ring_len);
+  return check(hipGetLastError(), "greedy_advance");
+}
+
+int cpi_hip_prompt_advance(const int* prompt, int n, int* token, int* position, cpi_stream_t s) {
+  if (!prompt || !token || !position || n <= 0) return fail("prompt_advance: bad arguments");
+  hipLaunchKernelGGL(cpi::prompt_advance_kernel, dim3(1), dim3(1), 0, S(s), prompt, n, token,
+                     position);
+  return check(hipGetLastError(), "prompt_advance");
+}
+
 int cpi_hip_quantize_rowwise_fp16_to_int8(const uint16_t* src, int8_t* dst, float* scales,
                                           int rows, int cols, int max_q, cpi_stream_t s) {
   if (!src || !dst || !scales || rows <= 0 || cols <= 0 || max_q <= 0 || max_q > 127)

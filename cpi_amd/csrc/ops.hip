@@ -186,6 +186,12 @@ __global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* x, in
   }
 }
 
+__global__ void prompt_advance_kernel(const int* prompt, int n, int* token, int* position) {
+  const int p = *position + 1;
+  *position = p;
+  if (p < n) *token = prompt[p];
+}
+
 // ---- quantise / pack / dequant (kernels_ops_matvec.cu:225-327, 449-487)
 __global__ void __launch_bounds__(256) quantize_rowwise_kernel(const uint16_t* src, int8_t* dst,
                                                                float* scales, int cols, int max_q) {

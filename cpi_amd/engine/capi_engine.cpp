@@ -1,0 +1,119 @@
+// C-ABI over engine::LlamaEngine (include/cpi_engine.h).
+#include <cstring>
+#include <exception>
+#include <string>
+
+#include "cpi_engine.h"
+#include "llama_engine.hpp"
+
+struct cpi_engine {
+  engine::LlamaEngine eng;
+};
+
+namespace {
+thread_local std::string g_err;
+int fail(const std::exception& e) {
+  g_err = e.what();
+  return -1;
+}
+}  // namespace
+
+extern "C" {
+
+void cpi_engine_default_options(cpi_engine_options* o) {
+  engine::EngineOptions d;
+  o->model_path = nullptr;
+  o->max_context = d.max_context;
+  o->rope_theta = d.rope_theta;
+  o->eos_token_id = d.eos_token_id;
+  o->loop_guard = d.loop_guard ? 1 : 0;
+  o->top_k = d.top_k;
+  o->top_p = d.top_p;
+  o->repetition_penalty = d.repetition_penalty;
+  o->verbose = d.verbose ? 1 : 0;
+  o->profile_decode_phases = 0;
+  o->graph_steps = d.graph_steps;
+}
+
+const char* cpi_engine_last_error(void) { return g_err.c_str(); }
+
+cpi_engine* cpi_engine_create(const cpi_engine_options* o) {
+  if (!o || !o->model_path) {
+    g_err = "[llama_engine] null options or model path";
+    return nullptr;
+  }
+  auto* e = new cpi_engine;
+  try {
+    engine::EngineOptions opt;
+    opt.model_path = o->model_path;
+    opt.max_context = o->max_context;
+    opt.rope_theta = o->rope_theta;
+    opt.eos_token_id = o->eos_token_id;
+    opt.loop_guard = o->loop_guard != 0;
+    opt.top_k = o->top_k;
+    opt.top_p = o->top_p;
+    opt.repetition_penalty = o->repetition_penalty;
+    opt.verbose = o->verbose != 0;
+    opt.profile_decode_phases = o->profile_decode_phases != 0;
+    opt.graph_steps = o->graph_steps;
+    e->eng.initialize(opt);
+  } catch (const std::exception& ex) {
+    fail(ex);
+    delete e;
+    return nullptr;
+  }
+  return e;
+}
+
+void cpi_engine_destroy(cpi_engine* e) { delete e; }
+
+int cpi_engine_generate(cpi_engine* e, const int* prompt, int n_prompt, int max_new, float temperature,
+                        int* out_ids, int* n_out, float* out_logits, int n_logit_steps) {
+  try {
+    std::vector<int> p(prompt, prompt + (n_prompt > 0 ? n_prompt : 0));
+    e->eng.set_logit_capture(out_logits, out_logits ? n_logit_steps : 0);
+    const std::vector<int> out = e->eng.generate(p, max_new, temperature);
+    e->eng.set_logit_capture(nullptr, 0);
+    const int gen = static_cast<int>(out.size()) - static_cast<int>(p.size());
+    for (int i = 0; i < gen && i < max_new; ++i) out_ids[i] = out[p.size() + static_cast<std::size_t>(i)];
+    if (n_out) *n_out = gen;
+    return 0;
+  } catch (const std::exception& ex) {
+    e->eng.set_logit_capture(nullptr, 0);
+    return fail(ex);
+  }
+}
+
+int cpi_engine_next_logits(cpi_engine* e, const int* prompt, int n_prompt, float* out_logits) {
+  try {
+    const std::vector<float> lg = e->eng.next_logits(std::vector<int>(prompt, prompt + n_prompt));
+    std::memcpy(out_logits, lg.data(), lg.size() * sizeof(float));
+    return 0;
+  } catch (const std::exception& ex) {
+    return fail(ex);
+  }
+}
+
+int cpi_engine_stats(const cpi_engine* e, cpi_benchmark_stats* o) {
+  const auto& s = e->eng.last_benchmark_stats();
+  o->prefill_ms = s.prefill_ms; o->decode_ms = s.decode_ms; o->transfer_ms = s.transfer_ms;
+  o->decode_rmsnorm_ms = s.decode_rmsnorm_ms; o->decode_qkv_ms = s.decode_qkv_ms;
+  o->decode_kv_store_ms = s.decode_kv_store_ms; o->decode_attention_ms = s.decode_attention_ms;
+  o->decode_wo_ms = s.decode_wo_ms; o->decode_mlp_ms = s.decode_mlp_ms;
+  o->decode_moe_router_ms = s.decode_moe_router_ms; o->decode_moe_expert_ms = s.decode_moe_expert_ms;
+  o->decode_moe_merge_ms = s.decode_moe_merge_ms; o->decode_lm_head_ms = s.decode_lm_head_ms;
+  o->prompt_tokens = s.prompt_tokens; o->generated_tokens = s.generated_tokens;
+  o->streamed_layer_copies = s.streamed_layer_copies; o->tq3_cached_active = s.tq3_cached_active;
+  return 0;
+}
+
+int cpi_engine_dims(const cpi_engine* e, int* o) {
+  const auto& c = e->eng.config();
+  o[0] = c.vocab_size; o[1] = c.hidden_size; o[2] = c.intermediate_size; o[3] = c.num_layers;
+  o[4] = c.num_heads; o[5] = c.num_kv_heads; o[6] = e->eng.head_dim(); o[7] = e->eng.max_context();
+  return 0;
+}
+
+size_t cpi_engine_weight_bytes(const cpi_engine* e) { return e->eng.weight_bytes(); }
+
+}  // extern "C"

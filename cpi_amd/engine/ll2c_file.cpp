@@ -1,0 +1,136 @@
+#include "ll2c_file.hpp"
+
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cstring>
+#include <stdexcept>
+
+#define LL2C_THROW(msg) throw std::runtime_error(std::string("[llama_engine] ") + (msg))
+
+namespace model {
+namespace {
+
+// Header field offsets (packed little-endian; weight_loader.cpp:10-94).
+struct Raw {
+  const std::byte* p;
+  std::int32_t i32(std::size_t off) const {
+    std::int32_t v;
+    std::memcpy(&v, p + off, 4);
+    return v;
+  }
+  float f32(std::size_t off) const {
+    float v;
+    std::memcpy(&v, p + off, 4);
+    return v;
+  }
+  std::int64_t i64(std::size_t off) const {
+    std::int64_t v;
+    std::memcpy(&v, p + off, 8);
+    return v;
+  }
+};
+
+constexpr std::size_t kHeaderV1 = 52, kHeaderV2 = 56, kHeaderV3 = 76, kHeaderV4 = 88;
+constexpr std::size_t kEntry = 80;
+
+}  // namespace
+
+LL2CFile::~LL2CFile() {
+  if (base_) munmap(const_cast<std::byte*>(base_), size_);
+}
+
+void LL2CFile::open(const std::string& path) {
+  const int fd = ::open(path.c_str(), O_RDONLY);
+  if (fd < 0) LL2C_THROW("cannot open model file: " + path);
+  struct stat st {};
+  if (fstat(fd, &st) != 0) {
+    ::close(fd);
+    LL2C_THROW("cannot stat model file: " + path);
+  }
+  size_ = static_cast<std::size_t>(st.st_size);
+  void* m = mmap(nullptr, size_, PROT_READ, MAP_PRIVATE, fd, 0);
+  ::close(fd);
+  if (m == MAP_FAILED) LL2C_THROW("mmap failed: " + path);
+  base_ = static_cast<const std::byte*>(m);
+  madvise(m, size_, MADV_WILLNEED);  // mmap_file.cpp:94,103-117
+  parse();
+}
+
+void LL2CFile::parse() {
+  if (size_ < kHeaderV1) LL2C_THROW("invalid model file");
+  if (std::memcmp(base_, "LL2CUDA", 7) != 0)
+    LL2C_THROW("unsupported weights format. expected LL2CUDA manifest");
+  const Raw r{base_};
+  const int version = r.i32(8);
+  LlamaConfig& c = config_;
+  c.vocab_size = r.i32(12);
+  c.hidden_size = r.i32(16);
+  c.intermediate_size = r.i32(20);
+  c.num_layers = r.i32(24);
+  c.num_heads = r.i32(28);
+  std::int32_t count = 0;
+  std::int64_t table = 0;
+  if (version >= 2) {
+    const std::size_t need = version >= 4 ? kHeaderV4 : (version >= 3 ? kHeaderV3 : kHeaderV2);
+    if (size_ < need) LL2C_THROW("invalid v" + std::to_string(version) + " model header");
+    c.num_kv_heads = r.i32(32);
+    c.max_seq_len = r.i32(36);
+    c.tensor_parallel = r.i32(40);
+    count = r.i32(44);
+    table = r.i64(48);
+    if (version >= 3) {
+      c.rope_theta = r.f32(56);
+      const float eps = r.f32(60);
+      c.norm_eps = eps > 0.0f ? eps : 1e-5f;
+      c.sliding_window = r.i32(64);
+      const std::int32_t flags = r.i32(68);
+      c.tie_word_embeddings = (flags & 1) != 0;
+      c.has_qkv_bias = (flags & 2) != 0;
+      c.use_layernorm = (flags & 4) != 0;
+      c.model_family = static_cast<ModelFamily>(r.i32(72));
+    }
+    if (version >= 4) {
+      c.num_local_experts = r.i32(76);
+      c.num_experts_per_tok = r.i32(80);
+      c.expert_intermediate_size = r.i32(84);
+    }
+  } else {
+    c.num_kv_heads = c.num_heads;
+    c.max_seq_len = r.i32(32);
+    c.tensor_parallel = r.i32(36);
+    count = r.i32(40);
+    table = r.i64(44);
+  }
+  if (c.num_kv_heads <= 0 || c.num_heads <= 0 || c.num_heads % c.num_kv_heads != 0)
+    LL2C_THROW("invalid attention head config in model header");
+  if (table < 0 || count < 0 || static_cast<std::size_t>(table) + count * kEntry > size_)
+    LL2C_THROW("tensor table out of range");
+  tensors_.clear();
+  for (int i = 0; i < count; ++i) {
+    const std::byte* e = base_ + table + static_cast<std::size_t>(i) * kEntry;
+    const char* nm = reinterpret_cast<const char*>(e);
+    const std::string name(nm, strnlen(nm, 64));
+    const std::int64_t off = r.i64(table + static_cast<std::size_t>(i) * kEntry + 64);
+    const std::int64_t bytes = r.i64(table + static_cast<std::size_t>(i) * kEntry + 72);
+    if (off < 0 || bytes < 0 || static_cast<std::size_t>(off + bytes) > size_)
+      LL2C_THROW("tensor out of file bounds: " + name);
+    tensors_[name] = TensorSlice{static_cast<std::size_t>(off), static_cast<std::size_t>(bytes)};
+  }
+}
+
+const std::byte* LL2CFile::tensor_data(const std::string& name) const {
+  const auto it = tensors_.find(name);
+  if (it == tensors_.end()) LL2C_THROW("tensor not found: " + name);
+  return base_ + it->second.offset;
+}
+
+std::size_t LL2CFile::tensor_bytes(const std::string& name) const {
+  const auto it = tensors_.find(name);
+  if (it == tensors_.end()) LL2C_THROW("tensor not found: " + name);
+  return it->second.bytes;
+}
+
+}  // namespace model

@@ -1,0 +1,81 @@
+// Memory-mapped .ll2c reader: model::WeightLoader + model::LlamaConfig of
+// kurulav1/cpi (include/model/weight_loader.hpp:27-59,
+// include/model/llama_config.hpp:39-76, src/model/weight_loader.cpp:10-242).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+#include <unordered_map>
+
+namespace model {
+
+enum class ModelFamily : std::int32_t {
+  Unknown = 0, LLaMA2 = 1, LLaMA3 = 2, Mistral = 3, Phi3 = 4, Qwen2 = 5, Mixtral = 6,
+};
+
+inline float default_rope_theta(ModelFamily f) {
+  switch (f) {
+    case ModelFamily::LLaMA3: return 500000.0f;
+    case ModelFamily::Qwen2: return 1000000.0f;
+    default: return 10000.0f;
+  }
+}
+
+struct LlamaConfig {
+  std::int32_t vocab_size = 32000;
+  std::int32_t hidden_size = 4096;
+  std::int32_t intermediate_size = 11008;
+  std::int32_t num_layers = 32;
+  std::int32_t num_heads = 32;
+  std::int32_t num_kv_heads = 32;
+  std::int32_t max_seq_len = 4096;
+  std::int32_t tensor_parallel = 1;
+  std::string dtype = "fp16";
+  ModelFamily model_family = ModelFamily::Unknown;
+  float rope_theta = 0.0f;
+  float norm_eps = 1e-5f;
+  std::int32_t sliding_window = 0;
+  bool has_qkv_bias = false;
+  bool use_layernorm = false;
+  bool tie_word_embeddings = false;
+  std::int32_t num_local_experts = 0;
+  std::int32_t num_experts_per_tok = 0;
+  std::int32_t expert_intermediate_size = 0;
+
+  float effective_rope_theta() const {
+    return rope_theta > 0.0f ? rope_theta : default_rope_theta(model_family);
+  }
+  bool is_moe() const { return num_local_experts > 0; }
+  std::int32_t effective_expert_intermediate_size() const {
+    return expert_intermediate_size > 0 ? expert_intermediate_size : intermediate_size;
+  }
+};
+
+struct TensorSlice {
+  std::size_t offset = 0;
+  std::size_t bytes = 0;
+};
+
+class LL2CFile {
+ public:
+  LL2CFile() = default;
+  LL2CFile(const LL2CFile&) = delete;
+  LL2CFile& operator=(const LL2CFile&) = delete;
+  ~LL2CFile();
+
+  void open(const std::string& path);  // throws std::runtime_error
+  const std::byte* tensor_data(const std::string& name) const;
+  std::size_t tensor_bytes(const std::string& name) const;
+  bool has_tensor(const std::string& name) const { return tensors_.count(name) != 0; }
+  const LlamaConfig& config() const { return config_; }
+
+ private:
+  void parse();
+  const std::byte* base_ = nullptr;
+  std::size_t size_ = 0;
+  LlamaConfig config_{};
+  std::unordered_map<std::string, TensorSlice> tensors_;
+};
+
+}  // namespace model

@@ -1,0 +1,547 @@
+// Resident decode engine: weight residency, the per-token launch sequence, the
+// hipGraph-captured greedy loop and host-side sampling.
+//
+// Reference behaviour followed (kurulav1/cpi):
+//   initialize ............. src/engine/llama_engine.cpp:974-1121
+//   per-token sequence ..... src/engine/llama_engine_graph.cpp:166-480
+//   prefill + generate ..... src/engine/llama_engine_generation.cpp:25-37,456-545
+//   greedy / sampling ...... src/engine/llama_engine_sampling.cpp:6-35,
+//                            src/engine/llama_engine_sampling_utils.cpp:10-264
+#include "llama_engine.hpp"
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <iostream>
+#include <numeric>
+#include <random>
+#include <stdexcept>
+
+#include "cpi_hip.h"
+
+#define ENGINE_THROW(msg) throw std::runtime_error(std::string("[llama_engine] ") + (msg))
+#define HIP_OK(expr)                                                                       \
+  do {                                                                                     \
+    hipError_t e_ = (expr);                                                                \
+    if (e_ != hipSuccess)                                                                  \
+      ENGINE_THROW(std::string(__FILE__) + ":" + std::to_string(__LINE__) + " HIP error: " + \
+                   hipGetErrorString(e_));                                                 \
+  } while (0)
+#define CPI_OK(expr)                                                                      \
+  do {                                                                                    \
+    if ((expr) != 0) ENGINE_THROW(std::string(#expr) + ": " + cpi_hip_last_error_string()); \
+  } while (0)
+
+namespace engine {
+namespace {
+
+using Clock = std::chrono::steady_clock;
+double ms_since(Clock::time_point t0) {
+  return std::chrono::duration<double, std::milli>(Clock::now() - t0).count();
+}
+
+// llama_engine_sampling_utils.cpp:191-242
+bool has_degenerate_tail(const std::vector<int>& ids, std::size_t prompt_size) {
+  if (ids.size() <= prompt_size + 8) return false;
+  const std::size_t gen = ids.size() - prompt_size;
+  const std::size_t n = ids.size();
+  auto repeats = [&](std::size_t period, std::size_t count) {
+    for (std::size_t i = 0; i < count; ++i)
+      if (ids[n - 1 - i] != ids[n - 1 - i - period]) return false;
+    return true;
+  };
+  if (gen >= 6) {
+    bool same = true;
+    for (std::size_t i = 1; i < 6; ++i) same = same && ids[n - 1 - i] == ids[n - 1];
+    if (same) return true;
+  }
+  if (gen >= 12 && repeats(2, 6)) return true;
+  if (gen >= 16 && repeats(4, 4)) return true;
+  return false;
+}
+
+}  // namespace
+
+LlamaEngine::~LlamaEngine() {
+  for (hipGraphExec_t g : {g_decode_many_, g_decode_one_, g_prefill_many_, g_prefill_one_})
+    if (g) (void)hipGraphExecDestroy(g);
+  for (void* p : allocations_) (void)hipFree(p);
+  if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void* LlamaEngine::dmalloc(std::size_t bytes) {
+  void* p = nullptr;
+  HIP_OK(hipMalloc(&p, bytes < 256 ? 256 : bytes));
+  allocations_.push_back(p);
+  return p;
+}
+
+uint16_t* LlamaEngine::upload_f16(const std::string& name, std::size_t expect_bytes) {
+  if (file_.tensor_bytes(name) != expect_bytes)
+    ENGINE_THROW("unexpected size for " + name + ": " + std::to_string(file_.tensor_bytes(name)) +
+                 " != " + std::to_string(expect_bytes));
+  auto* d = static_cast<uint16_t*>(dmalloc(expect_bytes));
+  HIP_OK(hipMemcpy(d, file_.tensor_data(name), expect_bytes, hipMemcpyHostToDevice));
+  weight_bytes_ += expect_bytes;
+  return d;
+}
+
+// Resolves "<name>" (fp16) or its low-bit variants: ".int8"/".int4" + ".scale"
+// (llama_engine_lowbit_utils.cpp:25-29) or ".int4" + ".gscale" (group-32).
+LlamaEngine::HostLinear LlamaEngine::bind_linear(const std::string& name, int rows, int cols) const {
+  HostLinear h;
+  h.rows = rows;
+  h.cols = cols;
+  auto need = [&](const std::string& n, std::size_t bytes) {
+    if (file_.tensor_bytes(n) != bytes)
+      ENGINE_THROW("unexpected size for " + n + ": " + std::to_string(file_.tensor_bytes(n)) +
+                   " != " + std::to_string(bytes));
+  };
+  const std::size_t R = static_cast<std::size_t>(rows), K = static_cast<std::size_t>(cols);
+  if (file_.has_tensor(name)) {
+    h.wfmt = CPI_W_F16;
+    need(name, R * K * 2);
+    h.w = file_.tensor_data(name);
+    h.w_bytes = R * K * 2;
+    return h;
+  }
+  if (file_.has_tensor(name + ".int4") && file_.has_tensor(name + ".gscale")) {
+    h.wfmt = CPI_W_I4G32;
+    need(name + ".int4", R * ((K + 1) / 2));
+    need(name + ".gscale", R * ((K + 31) / 32) * 2);
+    h.w = file_.tensor_data(name + ".int4");
+    h.w_bytes = R * ((K + 1) / 2);
+    h.scales = file_.tensor_data(name + ".gscale");
+    h.scale_bytes = R * ((K + 31) / 32) * 2;
+    return h;
+  }
+  const bool i8 = file_.has_tensor(name + ".int8");
+  const bool i4 = file_.has_tensor(name + ".int4");
+  if ((!i8 && !i4) || !file_.has_tensor(name + ".scale"))
+    ENGINE_THROW("tensor not found: " + name + " (and no INT8/INT4 alternative)");
+  h.wfmt = i8 ? CPI_W_I8ROW : CPI_W_I4ROW;
+  h.w_bytes = i8 ? R * K : R * ((K + 1) / 2);
+  need(name + (i8 ? ".int8" : ".int4"), h.w_bytes);
+  h.w = file_.tensor_data(name + (i8 ? ".int8" : ".int4"));
+  h.scales = file_.tensor_data(name + ".scale");
+  h.scale_bytes = file_.tensor_bytes(name + ".scale");
+  if (h.scale_bytes != 4 && h.scale_bytes != R * 4)
+    ENGINE_THROW("scale tensor of " + name + " must hold 1 or rows fp32 values");
+  return h;
+}
+
+// Concatenates the row blocks of `parts` (same format, same K) and stores them
+// on the device in the row order `order` (device row i = logical row order[i]).
+LlamaEngine::Linear LlamaEngine::upload_fused(const std::vector<HostLinear>& parts,
+                                              const std::vector<int>& order) {
+  Linear L;
+  L.wfmt = parts[0].wfmt;
+  L.cols = parts[0].cols;
+  for (const auto& p : parts) {
+    if (p.wfmt != L.wfmt || p.cols != L.cols) ENGINE_THROW("fused projections need one format and width");
+    L.rows += p.rows;
+  }
+  const std::size_t K = static_cast<std::size_t>(L.cols);
+  const std::size_t row_bytes = L.wfmt == CPI_W_F16 ? 2 * K : (L.wfmt == CPI_W_I8ROW ? K : (K + 1) / 2);
+  const std::size_t total = row_bytes * L.rows;
+  const bool identity = order.empty();
+
+  int* d_order = nullptr;
+  if (!identity) {
+    if (static_cast<int>(order.size()) != L.rows) ENGINE_THROW("row order size mismatch");
+    HIP_OK(hipMalloc(&d_order, order.size() * sizeof(int)));
+    HIP_OK(hipMemcpy(d_order, order.data(), order.size() * sizeof(int), hipMemcpyHostToDevice));
+  }
+  auto place = [&](const std::vector<std::pair<const std::byte*, std::size_t>>& blocks,
+                   std::size_t rb) -> void* {
+    void* dst = dmalloc(rb * L.rows);
+    void* stage = dst;
+    if (!identity) HIP_OK(hipMalloc(&stage, rb * L.rows));
+    std::size_t off = 0;
+    for (const auto& b : blocks) {
+      HIP_OK(hipMemcpy(static_cast<char*>(stage) + off, b.first, b.second, hipMemcpyHostToDevice));
+      off += b.second;
+    }
+    if (!identity) {
+      CPI_OK(cpi_hip_gather_rows(stage, dst, d_order, L.rows, rb, stream_));
+      HIP_OK(hipStreamSynchronize(stream_));
+      HIP_OK(hipFree(stage));
+    }
+    weight_bytes_ += rb * L.rows;
+    return dst;
+  };
+  std::vector<std::pair<const std::byte*, std::size_t>> wblocks;
+  for (const auto& p : parts) wblocks.push_back({p.w, p.w_bytes});
+  L.w = place(wblocks, row_bytes);
+  (void)total;
+
+  if (L.wfmt == CPI_W_I4G32) {
+    std::vector<std::pair<const std::byte*, std::size_t>> sblocks;
+    for (const auto& p : parts) sblocks.push_back({p.scales, p.scale_bytes});
+    L.scales = place(sblocks, ((K + 31) / 32) * 2);
+    L.scale_count = L.rows * static_cast<int>((K + 31) / 32);
+  } else if (L.wfmt != CPI_W_F16) {
+    // per-row fp32 scales (a single global scale is expanded per row)
+    std::vector<float> s;
+    s.reserve(L.rows);
+    for (const auto& p : parts) {
+      const float* src = reinterpret_cast<const float*>(p.scales);
+      for (int r = 0; r < p.rows; ++r) {
+        float v;
+        std::memcpy(&v, p.scale_bytes == 4 ? src : src + r, 4);
+        s.push_back(v);
+      }
+    }
+    L.scales = place({{reinterpret_cast<const std::byte*>(s.data()), s.size() * 4}}, 4);
+    L.scale_count = L.rows;
+  }
+  if (d_order) HIP_OK(hipFree(d_order));
+  return L;
+}
+
+void LlamaEngine::initialize(const EngineOptions& options) {
+  const auto t0 = Clock::now();
+  opts_ = options;
+  if (opts_.max_batch != 1) ENGINE_THROW("max_batch != 1 is not supported");  // llama_engine.cpp:1005
+  if (opts_.tensor_parallel != 1) ENGINE_THROW("tensor_parallel > 1 is not supported on this engine");
+  if (opts_.kv_cache_int4 || opts_.paged_kv_cache || opts_.int8_streaming || opts_.enable_tq_cached)
+    ENGINE_THROW("int4 KV / paged KV / streaming / TurboQuant paths are not part of this engine");
+  if (opts_.max_context <= 0) ENGINE_THROW("max_context must be positive");
+  file_.open(opts_.model_path);
+  cfg_ = file_.config();
+  if (cfg_.use_layernorm || cfg_.has_qkv_bias) ENGINE_THROW("LayerNorm / QKV-bias models are not supported");
+  if (cfg_.is_moe()) ENGINE_THROW("MoE models are not supported by this engine yet");
+  const int H = cfg_.hidden_size, I = cfg_.intermediate_size, V = cfg_.vocab_size;
+  const int NL = cfg_.num_layers, NH = cfg_.num_heads, NKV = cfg_.num_kv_heads;
+
+  // q_dim / head_dim from wq (cpu_engine.cpp:823-840), any storage format
+  const std::string wq0 = "layers.0.attention.wq";
+  if (file_.has_tensor(wq0)) q_dim_ = static_cast<int>(file_.tensor_bytes(wq0) / (2 * static_cast<std::size_t>(H)));
+  else if (file_.has_tensor(wq0 + ".gscale"))
+    q_dim_ = static_cast<int>(file_.tensor_bytes(wq0 + ".gscale") / (2 * static_cast<std::size_t>((H + 31) / 32)));
+  else if (file_.has_tensor(wq0 + ".int8"))
+    q_dim_ = static_cast<int>(file_.tensor_bytes(wq0 + ".int8") / static_cast<std::size_t>(H));
+  else if (file_.has_tensor(wq0 + ".int4"))
+    q_dim_ = static_cast<int>(file_.tensor_bytes(wq0 + ".int4") / static_cast<std::size_t>((H + 1) / 2));
+  if (q_dim_ <= 0 || q_dim_ % NH != 0) ENGINE_THROW("invalid q_proj shape");
+  head_dim_ = q_dim_ / NH;
+  kv_dim_ = NKV * head_dim_;
+  theta_ = opts_.rope_theta > 0.0f ? opts_.rope_theta : cfg_.effective_rope_theta();
+  graph_steps_ = opts_.graph_steps > 0 ? opts_.graph_steps : 16;
+  ring_len_ = graph_steps_;
+
+  HIP_OK(hipSetDevice(0));
+  HIP_OK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+
+  // ---- static weights
+  emb_ = upload_f16("tok_embeddings.weight", static_cast<std::size_t>(V) * H * 2);
+  norm_out_ = upload_f16("norm.weight", static_cast<std::size_t>(H) * 2);
+  if (file_.has_tensor("output.weight") || file_.has_tensor("output.weight.int8") ||
+      file_.has_tensor("output.weight.int4")) {
+    lm_head_ = upload_fused({bind_linear("output.weight", V, H)}, {});
+  } else {  // tied embeddings
+    lm_head_.wfmt = CPI_W_F16;
+    lm_head_.w = emb_;
+    lm_head_.rows = V;
+    lm_head_.cols = H;
+  }
+
+  // ---- layers
+  std::vector<int> qkv_order(static_cast<std::size_t>(q_dim_ + 2 * kv_dim_));
+  CPI_OK(cpi_hip_qkv_row_order(NH, NKV, head_dim_, qkv_order.data()));
+  std::vector<int> glu_order(static_cast<std::size_t>(2 * I));
+  CPI_OK(cpi_hip_swiglu_row_order(I, glu_order.data()));
+  const std::size_t kv_bytes = static_cast<std::size_t>(opts_.max_context) * kv_dim_ * 2;
+  layers_.resize(static_cast<std::size_t>(NL));
+  for (int l = 0; l < NL; ++l) {
+    const std::string p = "layers." + std::to_string(l) + ".";
+    Layer& L = layers_[static_cast<std::size_t>(l)];
+    L.norm_att = upload_f16(p + "attention_norm.weight", static_cast<std::size_t>(H) * 2);
+    L.norm_ffn = upload_f16(p + "ffn_norm.weight", static_cast<std::size_t>(H) * 2);
+    if (file_.has_tensor(p + "attention.bo")) ENGINE_THROW("attention.bo bias is not supported");
+    L.qkv = upload_fused({bind_linear(p + "attention.wq", q_dim_, H), bind_linear(p + "attention.wk", kv_dim_, H),
+                          bind_linear(p + "attention.wv", kv_dim_, H)},
+                         qkv_order);
+    L.wo = upload_fused({bind_linear(p + "attention.wo", H, q_dim_)}, {});
+    L.w13 = upload_fused({bind_linear(p + "feed_forward.w1", I, H), bind_linear(p + "feed_forward.w3", I, H)},
+                         glu_order);
+    L.w2 = upload_fused({bind_linear(p + "feed_forward.w2", H, I)}, {});
+    L.k_cache = static_cast<uint16_t*>(dmalloc(kv_bytes));
+    L.v_cache = static_cast<uint16_t*>(dmalloc(kv_bytes));
+  }
+
+  // ---- RoPE tables (fp32 [max_ctx, hd/2]; llama_engine_lifecycle.cpp:270-296)
+  const std::size_t half = static_cast<std::size_t>(head_dim_ / 2);
+  std::vector<float> c(static_cast<std::size_t>(opts_.max_context) * half), s(c.size());
+  CPI_OK(cpi_rope_tables(opts_.max_context, head_dim_, theta_, c.data(), s.data()));
+  rope_cos_ = static_cast<float*>(dmalloc(c.size() * 4));
+  rope_sin_ = static_cast<float*>(dmalloc(s.size() * 4));
+  HIP_OK(hipMemcpy(rope_cos_, c.data(), c.size() * 4, hipMemcpyHostToDevice));
+  HIP_OK(hipMemcpy(rope_sin_, s.data(), s.size() * 4, hipMemcpyHostToDevice));
+
+  // ---- runtime buffers
+  x_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(H) * 4));
+  q_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(q_dim_) * 4));
+  att_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(q_dim_) * 4));
+  ff_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(I) * 4));
+  logits_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(V) * 4));
+  attn_scratch_ = static_cast<float*>(dmalloc(cpi_hip_attention_scratch_floats(NH, head_dim_) * 4));
+  d_token_ = static_cast<int*>(dmalloc(4));
+  d_pos_ = static_cast<int*>(dmalloc(4));
+  d_step_ = static_cast<int*>(dmalloc(4));
+  d_ring_ = static_cast<int*>(dmalloc(static_cast<std::size_t>(ring_len_) * 4));
+  prompt_cap_ = opts_.max_context;
+  d_prompt_ = static_cast<int*>(dmalloc(static_cast<std::size_t>(prompt_cap_) * 4));
+  HIP_OK(hipMemset(d_prompt_, 0, static_cast<std::size_t>(prompt_cap_) * 4));
+  HIP_OK(hipMemset(d_token_, 0, 4));
+  HIP_OK(hipMemset(d_pos_, 0, 4));
+  HIP_OK(hipMemset(d_step_, 0, 4));
+  HIP_OK(hipDeviceSynchronize());
+
+  build_graphs();
+  if (opts_.verbose) {
+    std::cout << "[engine] resident gfx950 decode: layers=" << NL << " hidden=" << H << " heads=" << NH
+              << " kv_heads=" << NKV << " head_dim=" << head_dim_ << " inter=" << I << " vocab=" << V
+              << " max_context=" << opts_.max_context << " rope_theta=" << theta_
+              << " weights_mb=" << (weight_bytes_ >> 20) << "\n";
+    std::cout << "[startup] phase=initialize ms=" << ms_since(t0) << "\n";
+  }
+}
+
+// One token: embedding -> L x (QKV+RoPE+KV store, attention, o_proj+residual,
+// w1|w3+SwiGLU, w2+residual) -> [final norm + lm_head + argmax/advance].
+void LlamaEngine::enqueue_step(bool with_head) {
+  const int H = cfg_.hidden_size, I = cfg_.intermediate_size;
+  CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_token_, x_, 1, H, stream_));
+  for (auto& L : layers_) {
+    cpi_gemv_desc d{};
+    d.wfmt = L.qkv.wfmt; d.w = L.qkv.w; d.scales = L.qkv.scales; d.scale_count = L.qkv.scale_count;
+    d.out_features = L.qkv.rows; d.in_features = H;
+    d.x = x_; d.x_is_f32 = 1; d.norm_w = L.norm_att; d.norm_eps = cfg_.norm_eps;
+    d.epilogue = CPI_EPI_QKV_ROPE; d.y = q_;
+    d.num_heads = cfg_.num_heads; d.num_kv_heads = cfg_.num_kv_heads; d.head_dim = head_dim_;
+    d.position = d_pos_; d.rope_cos = rope_cos_; d.rope_sin = rope_sin_;
+    d.k_cache = L.k_cache; d.v_cache = L.v_cache; d.max_context = opts_.max_context;
+    CPI_OK(cpi_hip_gemv(&d, stream_));
+
+    CPI_OK(cpi_hip_attention_decode(q_, 1, L.k_cache, L.v_cache, att_, 1, 0, d_pos_, cfg_.num_heads,
+                                    cfg_.num_kv_heads, head_dim_, opts_.max_context, cfg_.sliding_window,
+                                    attn_scratch_, stream_));
+
+    cpi_gemv_desc o{};
+    o.wfmt = L.wo.wfmt; o.w = L.wo.w; o.scales = L.wo.scales; o.scale_count = L.wo.scale_count;
+    o.out_features = H; o.in_features = q_dim_; o.x = att_; o.x_is_f32 = 1;
+    o.epilogue = CPI_EPI_RESID_ADD; o.y = x_;
+    CPI_OK(cpi_hip_gemv(&o, stream_));
+
+    cpi_gemv_desc g{};
+    g.wfmt = L.w13.wfmt; g.w = L.w13.w; g.scales = L.w13.scales; g.scale_count = L.w13.scale_count;
+    g.out_features = 2 * I; g.in_features = H; g.x = x_; g.x_is_f32 = 1;
+    g.norm_w = L.norm_ffn; g.norm_eps = cfg_.norm_eps; g.epilogue = CPI_EPI_SWIGLU; g.y = ff_;
+    CPI_OK(cpi_hip_gemv(&g, stream_));
+
+    cpi_gemv_desc w{};
+    w.wfmt = L.w2.wfmt; w.w = L.w2.w; w.scales = L.w2.scales; w.scale_count = L.w2.scale_count;
+    w.out_features = H; w.in_features = I; w.x = ff_; w.x_is_f32 = 1;
+    w.epilogue = CPI_EPI_RESID_ADD; w.y = x_;
+    CPI_OK(cpi_hip_gemv(&w, stream_));
+  }
+  if (with_head) {
+    cpi_gemv_desc h{};
+    h.wfmt = lm_head_.wfmt; h.w = lm_head_.w; h.scales = lm_head_.scales; h.scale_count = lm_head_.scale_count;
+    h.out_features = cfg_.vocab_size; h.in_features = H; h.x = x_; h.x_is_f32 = 1;
+    h.norm_w = norm_out_; h.norm_eps = cfg_.norm_eps; h.epilogue = CPI_EPI_STORE_F32; h.y = logits_;
+    CPI_OK(cpi_hip_gemv(&h, stream_));
+    CPI_OK(cpi_hip_greedy_advance(logits_, cfg_.vocab_size, d_token_, d_pos_, d_step_, d_ring_, ring_len_,
+                                  stream_));
+  } else {
+    CPI_OK(cpi_hip_prompt_advance(d_prompt_, prompt_cap_, d_token_, d_pos_, stream_));
+  }
+}
+
+void LlamaEngine::build_graphs() {
+  auto capture = [&](bool head, int steps) {
+    hipGraph_t g = nullptr;
+    HIP_OK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    for (int i = 0; i < steps; ++i) enqueue_step(head);
+    HIP_OK(hipStreamEndCapture(stream_, &g));
+    hipGraphExec_t ge = nullptr;
+    HIP_OK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    HIP_OK(hipGraphDestroy(g));
+    return ge;
+  };
+  g_decode_one_ = capture(true, 1);
+  g_decode_many_ = capture(true, graph_steps_);
+  g_prefill_one_ = capture(false, 1);
+  g_prefill_many_ = capture(false, graph_steps_);
+}
+
+void LlamaEngine::run_graph(hipGraphExec_t g) { HIP_OK(hipGraphLaunch(g, stream_)); }
+
+void LlamaEngine::reset_state(const std::vector<int>& prompt) {
+  const int n = static_cast<int>(prompt.size());
+  if (n > prompt_cap_) ENGINE_THROW("prompt longer than max_context");
+  for (int t : prompt)
+    if (t < 0 || t >= cfg_.vocab_size) ENGINE_THROW("prompt token id out of range: " + std::to_string(t));
+  if (n > 0) HIP_OK(hipMemcpyAsync(d_prompt_, prompt.data(), static_cast<std::size_t>(n) * 4, hipMemcpyHostToDevice, stream_));
+  const int zero = 0;
+  const int first = n > 0 ? prompt[0] : 1;  // BOS seed for an empty prompt (cpu_engine.cpp:1085-1088)
+  HIP_OK(hipMemcpyAsync(d_token_, &first, 4, hipMemcpyHostToDevice, stream_));
+  HIP_OK(hipMemcpyAsync(d_pos_, &zero, 4, hipMemcpyHostToDevice, stream_));
+  HIP_OK(hipMemcpyAsync(d_step_, &zero, 4, hipMemcpyHostToDevice, stream_));
+  HIP_OK(hipStreamSynchronize(stream_));
+}
+
+std::vector<int> LlamaEngine::generate(const std::vector<int>& prompt, int max_new, float temperature) {
+  return generate_stream(prompt, max_new, temperature, [](int) { return true; });
+}
+
+std::vector<int> LlamaEngine::generate_stream(const std::vector<int>& prompt_in, int max_new, float temperature,
+                                              const std::function<bool(int)>& on_token) {
+  stats_ = BenchmarkStats{};
+  std::vector<int> prompt = prompt_in;
+  if (static_cast<int>(prompt.size()) > opts_.max_context) prompt.resize(static_cast<std::size_t>(opts_.max_context));
+  stats_.prompt_tokens = static_cast<int>(prompt.size());
+  std::vector<int> out = prompt;
+  reset_state(prompt);
+
+  // ---- prefill positions [0, n-2] (the last prompt token is consumed by the
+  // first decode step, whose logits give the first generated id)
+  const auto tp = Clock::now();
+  int pos = 0;
+  const int n_pre = prompt.empty() ? 0 : static_cast<int>(prompt.size()) - 1;
+  while (pos < n_pre) {
+    if (n_pre - pos >= graph_steps_) {
+      run_graph(g_prefill_many_);
+      pos += graph_steps_;
+    } else {
+      run_graph(g_prefill_one_);
+      pos += 1;
+    }
+  }
+  HIP_OK(hipStreamSynchronize(stream_));
+  stats_.prefill_ms = ms_since(tp);
+
+  // ---- decode
+  const auto td = Clock::now();
+  const bool greedy = temperature < 1e-6f && opts_.repetition_penalty == 1.0f;
+  const bool capture_logits = capture_ != nullptr && capture_steps_ > 0;
+  std::vector<int> ring(static_cast<std::size_t>(ring_len_));
+  std::vector<int> history;
+  int step = 0;
+  bool stop = false;
+  while (!stop && step < max_new) {
+    if (pos >= opts_.max_context) break;
+    const int left = std::min(max_new - step, opts_.max_context - pos);
+    const bool batch = greedy && !capture_logits && left >= graph_steps_;
+    const int n = batch ? graph_steps_ : 1;
+    run_graph(batch ? g_decode_many_ : g_decode_one_);
+    int ids[1] = {0};
+    if (greedy) {
+      HIP_OK(hipMemcpyAsync(ring.data(), d_ring_, static_cast<std::size_t>(ring_len_) * 4, hipMemcpyDeviceToHost, stream_));
+      HIP_OK(hipStreamSynchronize(stream_));
+      if (capture_logits && step < capture_steps_)
+        HIP_OK(hipMemcpy(capture_ + static_cast<std::size_t>(step) * cfg_.vocab_size, logits_,
+                         static_cast<std::size_t>(cfg_.vocab_size) * 4, hipMemcpyDeviceToHost));
+    } else {
+      HIP_OK(hipStreamSynchronize(stream_));
+      ids[0] = sample_host(temperature, history);
+      HIP_OK(hipMemcpyAsync(d_token_, ids, 4, hipMemcpyHostToDevice, stream_));
+    }
+    for (int i = 0; i < n && !stop; ++i) {
+      const int tok = greedy ? ring[static_cast<std::size_t>((step) % ring_len_)] : ids[0];
+      ++step;
+      ++pos;
+      out.push_back(tok);
+      history.push_back(tok);
+      ++stats_.generated_tokens;
+      if (opts_.eos_token_id >= 0 && tok == opts_.eos_token_id) stop = true;
+      else if (!on_token(tok)) stop = true;
+      else if (opts_.loop_guard && has_degenerate_tail(out, prompt.size())) stop = true;
+    }
+  }
+  HIP_OK(hipStreamSynchronize(stream_));
+  stats_.decode_ms = ms_since(td);
+  return out;
+}
+
+// Temperature / top-k / top-p / repetition penalty on host logits
+// (cpu_engine.cpp:709-764; llama_engine_sampling_utils.cpp:10-180).
+int LlamaEngine::sample_host(float temperature, const std::vector<int>& history) {
+  const int V = cfg_.vocab_size;
+  std::vector<float> lg(static_cast<std::size_t>(V));
+  HIP_OK(hipMemcpy(lg.data(), logits_, static_cast<std::size_t>(V) * 4, hipMemcpyDeviceToHost));
+  const float rp = opts_.repetition_penalty;
+  if (rp != 1.0f)
+    for (int id : history)
+      if (id >= 0 && id < V) lg[static_cast<std::size_t>(id)] = lg[static_cast<std::size_t>(id)] > 0.f ? lg[static_cast<std::size_t>(id)] / rp : lg[static_cast<std::size_t>(id)] * rp;
+  if (temperature < 1e-6f) return static_cast<int>(std::max_element(lg.begin(), lg.end()) - lg.begin());
+  for (float& v : lg) v /= temperature;
+  std::vector<int> idx(static_cast<std::size_t>(V));
+  std::iota(idx.begin(), idx.end(), 0);
+  int k = (opts_.top_k > 0 && opts_.top_k < V) ? opts_.top_k : V;
+  std::partial_sort(idx.begin(), idx.begin() + k, idx.end(),
+                    [&](int a, int b) { return lg[static_cast<std::size_t>(a)] > lg[static_cast<std::size_t>(b)]; });
+  idx.resize(static_cast<std::size_t>(k));
+  const float mx = lg[static_cast<std::size_t>(idx[0])];
+  std::vector<double> p(idx.size());
+  double sum = 0.0;
+  for (std::size_t i = 0; i < idx.size(); ++i) sum += p[i] = std::exp(static_cast<double>(lg[static_cast<std::size_t>(idx[i])] - mx));
+  std::size_t keep = idx.size();
+  if (opts_.top_p > 0.f && opts_.top_p < 1.f) {
+    double c = 0.0;
+    for (std::size_t i = 0; i < idx.size(); ++i) {
+      c += p[i] / sum;
+      if (c >= opts_.top_p) { keep = i + 1; break; }
+    }
+  }
+  double s2 = 0.0;
+  for (std::size_t i = 0; i < keep; ++i) s2 += p[i];
+  thread_local std::mt19937 rng{std::random_device{}()};
+  std::uniform_real_distribution<double> dist(0.0, s2);
+  double r = dist(rng), c = 0.0;
+  for (std::size_t i = 0; i < keep; ++i) {
+    c += p[i];
+    if (r <= c) return idx[i];
+  }
+  return idx[keep - 1];
+}
+
+std::vector<float> LlamaEngine::next_logits(const std::vector<int>& prompt) {
+  if (prompt.empty()) ENGINE_THROW("next_logits needs a non-empty prompt");
+  std::vector<float> out(static_cast<std::size_t>(cfg_.vocab_size));
+  float* keep = capture_;
+  const int keep_n = capture_steps_;
+  capture_ = out.data();
+  capture_steps_ = 1;
+  const bool lg = opts_.loop_guard;
+  const int eos = opts_.eos_token_id;
+  opts_.loop_guard = false;
+  opts_.eos_token_id = -1;
+  try {
+    generate(prompt, 1, 0.0f);
+  } catch (...) {
+    capture_ = keep; capture_steps_ = keep_n; opts_.loop_guard = lg; opts_.eos_token_id = eos;
+    throw;
+  }
+  capture_ = keep;
+  capture_steps_ = keep_n;
+  opts_.loop_guard = lg;
+  opts_.eos_token_id = eos;
+  return out;
+}
+
+std::vector<std::pair<int, float>> LlamaEngine::inspect_next_logits(const std::vector<int>& prompt, int top_k) {
+  const std::vector<float> lg = next_logits(prompt);
+  std::vector<std::pair<int, float>> pairs;
+  pairs.reserve(lg.size());
+  for (std::size_t i = 0; i < lg.size(); ++i) pairs.emplace_back(static_cast<int>(i), lg[i]);
+  const std::size_t k = std::min<std::size_t>(static_cast<std::size_t>(std::max(top_k, 0)), pairs.size());
+  std::partial_sort(pairs.begin(), pairs.begin() + k, pairs.end(),
+                    [](const auto& a, const auto& b) { return a.second > b.second; });
+  pairs.resize(k);
+  return pairs;
+}
+
+}  // namespace engine

@@ -1,0 +1,183 @@
+// Resident batch-1 decode engine for one MI355X.
+//
+// Same public surface as kurulav1/cpi engine::LlamaEngine
+// (include/engine/llama_engine.hpp:134-168); the CUDA/cuBLASLt internals are
+// replaced by the gfx950 kernels of libcpi_hip.so (include/cpi_hip.h).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <functional>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "ll2c_file.hpp"
+
+namespace engine {
+
+// engine::EngineOptions (llama_engine.hpp:65-98).  Fields of the reference
+// that select subsystems this engine does not have (layer streaming, TQ3,
+// int4 KV, paged KV) are kept for source compatibility and must stay at their
+// defaults; initialize() rejects anything else.
+struct EngineOptions {
+  std::string model_path;
+  int max_batch = 1;
+  int max_context = 2048;
+  int tensor_parallel = 1;
+  std::size_t vram_safety_margin_mb = 1024;
+  int gpu_cache_layers = -1;
+  std::size_t gpu_cache_limit_mb = 0;
+  bool gpu_cache_all = false;
+  int top_k = 40;
+  float top_p = 0.9f;
+  float repetition_penalty = 1.0f;
+  int no_repeat_ngram_size = 0;
+  bool int8_streaming = false;
+  int streaming_quant_bits = 8;
+  bool profile_decode_phases = false;
+  bool disable_split_attention = false;
+  bool loop_guard = true;
+  bool paged_kv_cache = false;
+  bool kv_cache_int4 = false;
+  bool enable_tq_cached = false;
+  std::string tq_mode = "auto";
+  bool verbose = true;
+  float rope_theta = 0.0f;
+  bool enable_host_resource_limits = true;
+  double max_cpu_percent = 85.0;
+  double max_memory_percent = 85.0;
+  int resource_sample_interval_ms = 250;
+  int resource_sustain_ms = 5000;
+  int resource_throttle_sleep_ms = 50;
+  int tq_cached_init_timeout_ms = 180000;
+  int tq_first_token_timeout_ms = 120000;
+  int eos_token_id = 2;
+  int graph_steps = 16;  // decode steps captured per graph launch (this engine)
+};
+
+// engine::BenchmarkStats (llama_engine.hpp:102-127).
+struct BenchmarkStats {
+  double prefill_ms = 0.0;
+  double decode_ms = 0.0;
+  double transfer_ms = 0.0;
+  double decode_rmsnorm_ms = 0.0;
+  double decode_qkv_ms = 0.0;
+  double decode_kv_store_ms = 0.0;
+  double decode_attention_ms = 0.0;
+  double decode_wo_ms = 0.0;
+  double decode_mlp_ms = 0.0;
+  double decode_moe_router_ms = 0.0;
+  double decode_moe_expert_ms = 0.0;
+  double decode_moe_merge_ms = 0.0;
+  double decode_lm_head_ms = 0.0;
+  int prompt_tokens = 0;
+  int generated_tokens = 0;
+  int streamed_layer_copies = 0;
+  int tq3_cached_active = 0;
+  int moe_topk_layers = 0;
+  int moe_topk_k = 0;
+  std::vector<int> moe_topk_indices{};
+  std::vector<float> moe_topk_probs{};
+  std::string moe_quant_mode = "none";
+};
+
+class LlamaEngine {
+ public:
+  LlamaEngine() = default;
+  LlamaEngine(const LlamaEngine&) = delete;
+  LlamaEngine& operator=(const LlamaEngine&) = delete;
+  ~LlamaEngine();
+
+  void initialize(const EngineOptions& options);
+
+  std::vector<int> generate(const std::vector<int>& prompt_tokens, int max_new_tokens,
+                            float temperature);
+  std::vector<int> generate_stream(const std::vector<int>& prompt_tokens, int max_new_tokens,
+                                   float temperature, const std::function<bool(int)>& on_token);
+  std::vector<std::pair<int, float>> inspect_next_logits(const std::vector<int>& prompt_tokens,
+                                                         int top_k);
+  const BenchmarkStats& last_benchmark_stats() const { return stats_; }
+
+  // Extensions used by the C-ABI / parity tests.
+  std::vector<float> next_logits(const std::vector<int>& prompt_tokens);
+  // When non-null, generate_stream copies the logits of the first n steps here.
+  void set_logit_capture(float* dst, int n_steps) { capture_ = dst; capture_steps_ = n_steps; }
+
+  const model::LlamaConfig& config() const { return cfg_; }
+  int head_dim() const { return head_dim_; }
+  int max_context() const { return opts_.max_context; }
+  std::size_t weight_bytes() const { return weight_bytes_; }
+
+ private:
+  // A (possibly fused) linear layer resident in device memory.
+  struct Linear {
+    int wfmt = 0;
+    void* w = nullptr;
+    void* scales = nullptr;
+    int scale_count = 0;
+    int rows = 0, cols = 0;
+  };
+  struct Layer {
+    Linear qkv, wo, w13, w2;
+    uint16_t* norm_att = nullptr;
+    uint16_t* norm_ffn = nullptr;
+    uint16_t* k_cache = nullptr;
+    uint16_t* v_cache = nullptr;
+  };
+
+  // host-side view of one stored linear (fp16 or low-bit + scales)
+  struct HostLinear {
+    int wfmt = 0;
+    const std::byte* w = nullptr;
+    std::size_t w_bytes = 0;
+    const std::byte* scales = nullptr;
+    std::size_t scale_bytes = 0;
+    int rows = 0, cols = 0;
+  };
+  HostLinear bind_linear(const std::string& name, int rows, int cols) const;
+  Linear upload_fused(const std::vector<HostLinear>& parts, const std::vector<int>& order);
+  void* dmalloc(std::size_t bytes);
+  uint16_t* upload_f16(const std::string& name, std::size_t expect_bytes);
+
+  void enqueue_step(bool with_head);
+  void build_graphs();
+  void run_graph(hipGraphExec_t g);
+  void reset_state(const std::vector<int>& prompt);
+  int sample_host(float temperature, const std::vector<int>& history);
+
+  EngineOptions opts_;
+  model::LL2CFile file_;
+  model::LlamaConfig cfg_;
+  int head_dim_ = 0, q_dim_ = 0, kv_dim_ = 0;
+  float theta_ = 10000.f;
+
+  hipStream_t stream_ = nullptr;
+  std::vector<void*> allocations_;
+  std::size_t weight_bytes_ = 0;
+  std::vector<Layer> layers_;
+  uint16_t* emb_ = nullptr;
+  uint16_t* norm_out_ = nullptr;
+  Linear lm_head_;
+  float *rope_cos_ = nullptr, *rope_sin_ = nullptr;
+
+  float *x_ = nullptr, *q_ = nullptr, *att_ = nullptr, *ff_ = nullptr, *logits_ = nullptr;
+  float* attn_scratch_ = nullptr;
+  int *d_token_ = nullptr, *d_pos_ = nullptr, *d_step_ = nullptr, *d_ring_ = nullptr,
+      *d_prompt_ = nullptr;
+  int ring_len_ = 16;
+  int prompt_cap_ = 0;
+  int n_prompt_dev_ = 1;
+
+  hipGraphExec_t g_decode_many_ = nullptr, g_decode_one_ = nullptr;
+  hipGraphExec_t g_prefill_many_ = nullptr, g_prefill_one_ = nullptr;
+  int graph_steps_ = 16;
+
+  float* capture_ = nullptr;
+  int capture_steps_ = 0;
+  BenchmarkStats stats_;
+};
+
+}  // namespace engine

@@ -1,0 +1,143 @@
+// llama_infer — command line front end with the reference's flag surface
+// (src/app/main_cli.cpp:84-348) and its [perf] / [bench] output lines
+// (src/app/main_modes.cpp:548-620).  Text prompts need a tokenizer, which is
+// outside this engine: pass token ids with --tokens.
+#include <chrono>
+#include <cstdlib>
+#include <iomanip>
+#include <iostream>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "llama_engine.hpp"
+
+namespace {
+
+void usage(std::ostream& os) {
+  os << "Usage: llama_infer <model.ll2c> --tokens csv [--max-new n] [--temp t] [--max-context n] "
+        "[--top-k n] [--top-p p] [--repeat-penalty r] [--rope-theta f] [--eos-token n] [--no-loop-guard] "
+        "[--benchmark] [--benchmark-reps n] [--benchmark-warmup n] [--benchmark-phases] [--runtime-metrics] "
+        "[--inspect-next-topk n] [--gpu-cache-all] [--no-resource-limits] [--graph-steps n] [--quiet]\n";
+}
+
+std::vector<int> parse_csv(const std::string& s) {
+  std::vector<int> v;
+  std::stringstream ss(s);
+  std::string tok;
+  while (std::getline(ss, tok, ','))
+    if (!tok.empty()) v.push_back(std::stoi(tok));
+  return v;
+}
+
+std::string env_or(const char* name, const std::string& d) {
+  const char* v = std::getenv(name);
+  return v && *v ? std::string(v) : d;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  if (argc < 2) {
+    usage(std::cerr);
+    return 2;
+  }
+  engine::EngineOptions opt;
+  // env overrides (main_cli.cpp:45-80)
+  opt.max_context = std::stoi(env_or("LLAMA_INFER_MAX_CONTEXT", std::to_string(opt.max_context)));
+  opt.top_k = std::stoi(env_or("LLAMA_INFER_TOP_K", std::to_string(opt.top_k)));
+  opt.top_p = std::stof(env_or("LLAMA_INFER_TOP_P", std::to_string(opt.top_p)));
+  opt.eos_token_id = std::stoi(env_or("LLAMA_INFER_EOS_TOKEN_ID", std::to_string(opt.eos_token_id)));
+
+  std::vector<int> tokens;
+  int max_new = 16, reps = 1, warmup = 0, inspect_k = 0;
+  float temp = 0.8f;
+  bool bench = false, phases = false, quiet = false;
+  opt.model_path = argv[1];
+  try {
+    for (int i = 2; i < argc; ++i) {
+      const std::string a = argv[i];
+      auto next = [&]() -> std::string {
+        if (i + 1 >= argc) throw std::runtime_error("missing value for " + a);
+        return argv[++i];
+      };
+      if (a == "--tokens") tokens = parse_csv(next());
+      else if (a == "--max-new") max_new = std::stoi(next());
+      else if (a == "--temp") temp = std::stof(next());
+      else if (a == "--max-context") opt.max_context = std::stoi(next());
+      else if (a == "--top-k") opt.top_k = std::stoi(next());
+      else if (a == "--top-p") opt.top_p = std::stof(next());
+      else if (a == "--repeat-penalty") opt.repetition_penalty = std::stof(next());
+      else if (a == "--rope-theta") opt.rope_theta = std::stof(next());
+      else if (a == "--eos-token") opt.eos_token_id = std::stoi(next());
+      else if (a == "--no-loop-guard") opt.loop_guard = false;
+      else if (a == "--benchmark") bench = true;
+      else if (a == "--benchmark-reps") reps = std::stoi(next());
+      else if (a == "--benchmark-warmup") warmup = std::stoi(next());
+      else if (a == "--benchmark-phases" || a == "--runtime-metrics") phases = true;
+      else if (a == "--inspect-next-topk") inspect_k = std::stoi(next());
+      else if (a == "--graph-steps") opt.graph_steps = std::stoi(next());
+      else if (a == "--quiet") quiet = true;
+      else if (a == "--gpu-cache-all" || a == "--no-resource-limits" || a == "--no-split-attention") {
+        // always fully resident; no host guardrails on this path
+      } else if (a == "--help" || a == "-h") {
+        usage(std::cout);
+        return 0;
+      } else if (a == "--prompt" || a == "--tokenizer" || a == "--cpu" || a == "--web" || a == "--interactive" ||
+                 a == "--int8-streaming" || a == "--int4-streaming" || a == "--kv-int4" ||
+                 a == "--paged-kv-cache" || a == "--enable-tq-cached" || a == "--parity-check") {
+        std::cerr << "[llama_infer] " << a << " is not supported by the MI355X decode engine\n";
+        return 2;
+      } else {
+        std::cerr << "[llama_infer] unknown flag " << a << "\n";
+        usage(std::cerr);
+        return 2;
+      }
+    }
+    opt.profile_decode_phases = phases;
+    opt.verbose = !quiet;
+    engine::LlamaEngine eng;
+    eng.initialize(opt);
+    if (inspect_k > 0) {
+      for (const auto& [id, v] : eng.inspect_next_logits(tokens, inspect_k))
+        std::cout << "[inspect] id=" << id << " logit=" << std::setprecision(6) << v << "\n";
+      return 0;
+    }
+    for (int w = 0; w < warmup; ++w) eng.generate(tokens, max_new, temp);
+    double sum_prefill = 0, sum_decode = 0, sum_total = 0, sum_gen = 0;
+    std::vector<int> out;
+    for (int r = 0; r < reps; ++r) {
+      const auto t0 = std::chrono::steady_clock::now();
+      out = eng.generate(tokens, max_new, temp);
+      const double ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+      const auto& s = eng.last_benchmark_stats();
+      sum_prefill += s.prefill_ms;
+      sum_decode += s.decode_ms;
+      sum_total += ms;
+      sum_gen += s.generated_tokens;
+    }
+    if (!quiet) {
+      std::cout << "Output tokens:";
+      for (std::size_t i = tokens.size(); i < out.size(); ++i) std::cout << (i == tokens.size() ? " " : ",") << out[i];
+      std::cout << "\n";
+    }
+    const auto& s = eng.last_benchmark_stats();
+    const double gen = sum_gen / reps, total = sum_total / reps;
+    std::cout << std::fixed << std::setprecision(2) << (reps > 1 ? "[perf-avg] " : "[perf] ")
+              << "generated_tokens=" << gen << " elapsed_ms=" << total
+              << " tok_per_s=" << (total > 0 ? 1000.0 * gen / total : 0.0) << "\n";
+    if (bench) {
+      const int pre = s.prompt_tokens > 0 ? s.prompt_tokens - 1 : 0;
+      const double pms = sum_prefill / reps, dms = sum_decode / reps;
+      std::cout << (reps > 1 ? "[bench-avg] reps=" + std::to_string(reps) + " " : "[bench] ")
+                << "prefill_tokens=" << pre << " prefill_ms=" << pms
+                << " prefill_tok_per_s=" << (pms > 0 ? 1000.0 * pre / pms : 0.0) << " decode_tokens=" << gen
+                << " decode_ms=" << dms << " decode_tok_per_s=" << (dms > 0 ? 1000.0 * gen / dms : 0.0)
+                << " transfer_ms=0.00 streamed_layer_copies=0 tq3_cached_active=0\n";
+    }
+  } catch (const std::exception& e) {
+    std::cerr << e.what() << "\n";
+    return 1;
+  }
+  return 0;
+}

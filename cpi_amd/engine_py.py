@@ -1,0 +1,110 @@
+"""ctypes binding of include/cpi_engine.h (libcpi_engine.so): the resident
+decode engine.  Raises if the library was not built; there is no fallback."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+from cpi_amd import _lib
+
+_eng = None
+
+
+class Options(ctypes.Structure):
+    _fields_ = [("model_path", ctypes.c_char_p), ("max_context", ctypes.c_int), ("rope_theta", ctypes.c_float),
+                ("eos_token_id", ctypes.c_int), ("loop_guard", ctypes.c_int), ("top_k", ctypes.c_int),
+                ("top_p", ctypes.c_float), ("repetition_penalty", ctypes.c_float), ("verbose", ctypes.c_int),
+                ("profile_decode_phases", ctypes.c_int), ("graph_steps", ctypes.c_int)]
+
+
+class Stats(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_double) for n in (
+        "prefill_ms", "decode_ms", "transfer_ms", "decode_rmsnorm_ms", "decode_qkv_ms", "decode_kv_store_ms",
+        "decode_attention_ms", "decode_wo_ms", "decode_mlp_ms", "decode_moe_router_ms", "decode_moe_expert_ms",
+        "decode_moe_merge_ms", "decode_lm_head_ms")] + [(n, ctypes.c_int) for n in (
+            "prompt_tokens", "generated_tokens", "streamed_layer_copies", "tq3_cached_active")]
+
+
+def lib():
+    global _eng
+    if _eng is None:
+        _lib.lib()  # libcpi_hip.so first (dependency)
+        if not os.path.exists(_lib.ENGINE_PATH):
+            raise _lib.CpiHipError(f"{_lib.ENGINE_PATH} is missing: run __graft_entry__.build()")
+        L = ctypes.CDLL(_lib.ENGINE_PATH)
+        P = ctypes.c_void_p
+        L.cpi_engine_default_options.argtypes = [ctypes.POINTER(Options)]
+        L.cpi_engine_last_error.restype = ctypes.c_char_p
+        L.cpi_engine_create.restype = P
+        L.cpi_engine_create.argtypes = [ctypes.POINTER(Options)]
+        L.cpi_engine_destroy.argtypes = [P]
+        L.cpi_engine_generate.restype = ctypes.c_int
+        L.cpi_engine_generate.argtypes = [P, P, ctypes.c_int, ctypes.c_int, ctypes.c_float, P, P, P, ctypes.c_int]
+        L.cpi_engine_next_logits.restype = ctypes.c_int
+        L.cpi_engine_next_logits.argtypes = [P, P, ctypes.c_int, P]
+        L.cpi_engine_stats.argtypes = [P, ctypes.POINTER(Stats)]
+        L.cpi_engine_dims.argtypes = [P, P]
+        L.cpi_engine_weight_bytes.restype = ctypes.c_size_t
+        L.cpi_engine_weight_bytes.argtypes = [P]
+        _eng = L
+    return _eng
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Engine:
+    def __init__(self, path: str, max_context: int = 2048, eos: int = 2, loop_guard: bool = True,
+                 graph_steps: int = 16, verbose: bool = False, rope_theta: float = 0.0):
+        o = Options()
+        lib().cpi_engine_default_options(ctypes.byref(o))
+        self._path = path.encode()
+        o.model_path, o.max_context, o.eos_token_id = self._path, max_context, eos
+        o.loop_guard, o.graph_steps, o.verbose, o.rope_theta = int(loop_guard), graph_steps, int(verbose), rope_theta
+        self.h = lib().cpi_engine_create(ctypes.byref(o))
+        if not self.h:
+            raise RuntimeError(lib().cpi_engine_last_error().decode())
+        d = np.zeros(8, np.int32)
+        lib().cpi_engine_dims(self.h, _ptr(d))
+        (self.vocab, self.hidden, self.inter, self.layers, self.heads, self.kv_heads, self.head_dim,
+         self.max_context) = (int(v) for v in d)
+
+    def generate(self, prompt, max_new: int, temperature: float = 0.0, logit_steps: int = 0):
+        p = np.ascontiguousarray(prompt, np.int32)
+        ids = np.zeros(max(max_new, 1), np.int32)
+        n = np.zeros(1, np.int32)
+        lg = np.zeros((max(logit_steps, 1), self.vocab), np.float32) if logit_steps else None
+        rc = lib().cpi_engine_generate(self.h, _ptr(p), p.size, max_new, temperature, _ptr(ids), _ptr(n),
+                                       _ptr(lg) if lg is not None else None, logit_steps)
+        if rc:
+            raise RuntimeError(lib().cpi_engine_last_error().decode())
+        return ids[: int(n[0])], (lg[:logit_steps] if lg is not None else None)
+
+    def next_logits(self, prompt):
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(self.vocab, np.float32)
+        if lib().cpi_engine_next_logits(self.h, _ptr(p), p.size, _ptr(out)):
+            raise RuntimeError(lib().cpi_engine_last_error().decode())
+        return out
+
+    def stats(self) -> dict:
+        s = Stats()
+        lib().cpi_engine_stats(self.h, ctypes.byref(s))
+        return {k: getattr(s, k) for k, _ in Stats._fields_}
+
+    def weight_bytes(self) -> int:
+        return int(lib().cpi_engine_weight_bytes(self.h))
+
+    def close(self):
+        if self.h:
+            lib().cpi_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

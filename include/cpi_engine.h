@@ -1,0 +1,77 @@
+/*
+ * cpi_engine.h — C-ABI of the resident batch-1 decode engine (libcpi_engine.so).
+ *
+ * The engine mirrors engine::LlamaEngine of kurulav1/cpi
+ * (include/engine/llama_engine.hpp:134-168: initialize, generate,
+ * generate_stream, inspect_next_logits, last_benchmark_stats) over an .ll2c
+ * file, fully resident on one MI355X, driving libcpi_hip.so.  The C++ class is
+ * cpi_amd/engine/llama_engine.hpp; this header is the FFI boundary used by
+ * the CLI, Python (ctypes) and any other host language.
+ *
+ * Functions return 0 on success, -1 on error; cpi_engine_last_error() gives
+ * the message ("[llama_engine] ..." like LLAMA_ENGINE_THROW, include/common.hpp:12).
+ */
+#ifndef CPI_ENGINE_H
+#define CPI_ENGINE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct cpi_engine cpi_engine;
+
+/* Subset of engine::EngineOptions (llama_engine.hpp:65-98) that affects the
+ * resident decode path; field meanings and defaults follow the reference. */
+typedef struct cpi_engine_options {
+  const char* model_path;
+  int max_context;          /* default 2048 */
+  float rope_theta;         /* 0 = from file / family default */
+  int eos_token_id;         /* default 2; -1 disables */
+  int loop_guard;           /* default 1 */
+  int top_k;                /* default 40 */
+  float top_p;              /* default 0.9 */
+  float repetition_penalty; /* default 1.0 */
+  int verbose;              /* default 1 */
+  int profile_decode_phases;/* default 0 */
+  int graph_steps;          /* decode steps per graph launch; 0 = default (16) */
+} cpi_engine_options;
+
+/* engine::BenchmarkStats (llama_engine.hpp:102-127), scalar fields. */
+typedef struct cpi_benchmark_stats {
+  double prefill_ms, decode_ms, transfer_ms;
+  double decode_rmsnorm_ms, decode_qkv_ms, decode_kv_store_ms, decode_attention_ms;
+  double decode_wo_ms, decode_mlp_ms, decode_moe_router_ms, decode_moe_expert_ms;
+  double decode_moe_merge_ms, decode_lm_head_ms;
+  int prompt_tokens, generated_tokens, streamed_layer_copies, tq3_cached_active;
+} cpi_benchmark_stats;
+
+void cpi_engine_default_options(cpi_engine_options* o);
+const char* cpi_engine_last_error(void);
+
+/* LlamaEngine::initialize */
+cpi_engine* cpi_engine_create(const cpi_engine_options* o);
+void cpi_engine_destroy(cpi_engine* e);
+
+/* LlamaEngine::generate: ids written to out_ids (capacity max_new); *n_out =
+ * number generated.  If out_logits != NULL, the fp32 logits each of the first
+ * n_logit_steps ids was taken from are written row-major [n_logit_steps, vocab]. */
+int cpi_engine_generate(cpi_engine* e, const int* prompt, int n_prompt, int max_new,
+                        float temperature, int* out_ids, int* n_out, float* out_logits,
+                        int n_logit_steps);
+
+/* LlamaEngine::inspect_next_logits: full next-token logits [vocab] after the prompt. */
+int cpi_engine_next_logits(cpi_engine* e, const int* prompt, int n_prompt, float* out_logits);
+
+int cpi_engine_stats(const cpi_engine* e, cpi_benchmark_stats* out);
+/* vocab, hidden, inter, layers, heads, kv_heads, head_dim, max_context */
+int cpi_engine_dims(const cpi_engine* e, int* out8);
+/* Bytes of device memory held by resident weights. */
+size_t cpi_engine_weight_bytes(const cpi_engine* e);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CPI_ENGINE_H */

@@ -245,6 +245,19 @@ int cpi_hip_moe_router_topk_softmax(const uint16_t* logits, int experts,
 /* launch_argmax_float (kernels.cuh:785-788): lowest index among maxima. */
 int cpi_hip_argmax_float(const float* logits, int n, int* out_index,
                          cpi_stream_t stream);
+/* Greedy step tail for the captured decode loop: token = argmax(logits)
+ * (lowest index among maxima), ring[*step % ring_len] = token, ++*step,
+ * ++*position.  Replaces argmax_float + copy_int + increment_int at
+ * src/engine/llama_engine_graph.cpp:472-474. */
+int cpi_hip_greedy_advance(const float* logits, int n, int* token, int* position,
+                           int* step, int* ring, int ring_len, cpi_stream_t stream);
+/* Prompt step tail (sequential prefill inside a graph): ++*position, then
+ * token = prompt[*position] when *position < n_prompt.  Replaces the host
+ * token/position copies of the per-token prefill loop
+ * (src/engine/llama_engine_generation.cpp:25-37). */
+int cpi_hip_prompt_advance(const int* prompt, int n_prompt, int* token, int* position,
+                           cpi_stream_t stream);
+
 /* launch_quantize_rowwise_fp16_to_int8 (kernels.cuh:490-496) */
 int cpi_hip_quantize_rowwise_fp16_to_int8(const uint16_t* src, int8_t* dst,
                                           float* scales, int rows, int cols,

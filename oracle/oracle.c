@@ -99,7 +99,13 @@ static void mat_row(const omat* m, int r, float* dst) {
   switch (m->fmt) {
     case OW_F16: {
       const uint16_t* row = (const uint16_t*)m->w + (size_t)r * K;
-      for (int j = 0; j < K; ++j) dst[j] = oracle_fp16_to_fp32(row[j]);
+      int j = 0;
+#ifdef ORACLE_AVX2
+      /* F16C conversion is exact, identical to oracle_fp16_to_fp32 */
+      for (; j + 8 <= K; j += 8)
+        _mm256_storeu_ps(dst + j, _mm256_cvtph_ps(_mm_loadu_si128((const __m128i*)(row + j))));
+#endif
+      for (; j < K; ++j) dst[j] = oracle_fp16_to_fp32(row[j]);
       break;
     }
     case OW_F32:

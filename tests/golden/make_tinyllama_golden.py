@@ -1,0 +1,48 @@
+"""Writes tests/golden/tinyllama_fp16_seed0.npz: greedy ids and logits of the
+CPU oracle (restatement of the reference CPU engine) on BASELINE config 1:
+
+TinyLlama-1.1B-shaped decoder, fp16, random-init N(0, 0.02^2) weights (norm
+weights 1.0), seed 0, theta 1e4, eps 1e-5, prompt = 128 ids uniform in
+[0, 32000) from numpy default_rng(0), 64 greedy tokens, EOS disabled.
+
+Usage: python tests/golden/make_tinyllama_golden.py [model_path]
+"""
+import os
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+sys.path.insert(0, ROOT)
+
+from cpi_amd import ll2c  # noqa: E402
+
+OUT = os.path.join(ROOT, "tests", "golden", "tinyllama_fp16_seed0.npz")
+LOGIT_STEPS = (0, 1, 15, 31)
+
+
+def spec():
+    return ll2c.SynthSpec(ll2c.tinyllama_config(), attn_fmt="f16", mlp_fmt="f16", seed=0, std=0.02)
+
+
+def prompt():
+    return np.random.default_rng(0).integers(0, 32000, 128).astype(np.int32)
+
+
+def main():
+    import oracle
+    path = sys.argv[1] if len(sys.argv) > 1 else os.path.join(tempfile.gettempdir(), "tinyllama_seed0.ll2c")
+    sha = ll2c.write_synthetic(path, spec())
+    eng = oracle.Engine(path, 256)
+    t0 = time.time()
+    ids, lg = eng.generate(prompt(), 64, eos=-1, logit_steps=32)
+    dt = time.time() - t0
+    np.savez(OUT, ids=ids.astype(np.int32), logit_steps=np.array(LOGIT_STEPS, np.int32),
+             logits=lg[list(LOGIT_STEPS)].astype(np.float16), model_sha256=np.array(sha))
+    print(f"wrote {OUT}: ids[:8]={ids[:8]} oracle {dt:.1f}s ({(128 + 64) / dt:.2f} tok/s) sha={sha}")
+
+
+if __name__ == "__main__":
+    main()
