@@ -33,6 +33,32 @@ CASES = {
 }
 
 
+def first_divergence(a, b):
+    """Number of leading ids that agree.  Logits are comparable only up to and
+    including that step: later steps consume different tokens."""
+    n = min(len(a), len(b))
+    d = np.nonzero(a[:n] != b[:n])[0]
+    return int(d[0]) + 1 if d.size else n
+
+
+def assert_ids_or_tie(n, ref_logits, err, need=32):
+    """Greedy ids must agree for `need` steps.  A split before that is accepted
+    only when it is a tie inside the measured numeric error: the oracle's top-2
+    margin at the split step is below 4x the largest logit error seen."""
+    if n >= need:
+        return
+    s = np.sort(ref_logits[n - 1])
+    margin = s[-1] - s[-2]
+    assert margin <= 4 * max(err, 1e-6), f"ids diverge at step {n - 1} with top-2 margin {margin:.3e} > 4*err"
+
+
+def margin_note(lg, n):
+    if n >= len(lg):
+        return ""
+    s = np.sort(lg[n - 1])
+    return f"(oracle top-2 margin at step {n - 1}: {s[-1] - s[-2]:.2e})"
+
+
 @pytest.mark.parametrize("name", list(CASES))
 def test_engine_matches_oracle(tmp_path, name):
     from cpi_amd.engine_py import Engine
@@ -46,10 +72,17 @@ def test_engine_matches_oracle(tmp_path, name):
     rids, rlg = ref.generate(prompt, 40, eos=-1, logit_steps=40)
     eng = Engine(path, max_context=128, eos=-1, loop_guard=False)
     ids, lg = eng.generate(prompt, 40, logit_steps=40)
-    err = np.abs(lg - rlg).max()
-    print(f"[engine] {name} max_abs_logit_err={err:.3e} ids_equal={int((ids == rids).sum())}/40", flush=True)
+    n = first_divergence(ids, rids)
+    err = np.abs(lg[:n] - rlg[:n]).max()
+    print(f"[engine] {name} max_abs_logit_err={err:.3e} identical_prefix={n}/40 {margin_note(rlg, n)}", flush=True)
     assert err <= LOGIT_TOL
-    assert (ids[:32] == rids[:32]).all()
+    assert_ids_or_tie(n, rlg, err)
+    # teacher-forced: the engine fed the oracle's ids reproduces the oracle's
+    # logits at every step, also past a tie-induced split
+    for k in (n, 31, 39):
+        if k < 40:
+            tf = eng.next_logits(np.concatenate([prompt, rids[:k]]))
+            assert np.abs(tf - rlg[k]).max() <= LOGIT_TOL, k
     # the batched greedy graph (16 steps per launch) gives the same ids as the
     # per-step path used for logit capture
     ids2, _ = eng.generate(prompt, 40)
@@ -92,9 +125,10 @@ def test_tinyllama_golden(tmp_path):
     assert sha == str(g["model_sha256"]), "synthetic model bytes differ from the fixture's"
     eng = Engine(path, max_context=256, eos=-1, loop_guard=False)
     ids, lg = eng.generate(mk.prompt(), 64, logit_steps=32)
-    steps = list(g["logit_steps"])
-    err = np.abs(lg[steps] - g["logits"].astype(np.float32)).max()
-    same = int((ids == g["ids"]).sum())
-    print(f"[tinyllama] max_abs_logit_err={err:.3e} ids_equal={same}/64", flush=True)
+    n = first_divergence(ids, g["ids"])
+    steps = [s for s in g["logit_steps"] if s < n]
+    idx = [list(g["logit_steps"]).index(s) for s in steps]
+    err = np.abs(lg[steps] - g["logits"][idx].astype(np.float32)).max()
+    print(f"[tinyllama] max_abs_logit_err={err:.3e} identical_prefix={n}/64", flush=True)
     assert err <= LOGIT_TOL
-    assert (ids[:32] == g["ids"][:32]).all()
+    assert n >= 32, "TinyLlama config-1 ids must match for 32 steps"
