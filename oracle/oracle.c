@@ -131,7 +131,19 @@ static void mat_row(const omat* m, int r, float* dst) {
       const int ng = (K + 31) / 32;
       const uint8_t* row = (const uint8_t*)m->w + (size_t)r * pc;
       const uint16_t* gs = (const uint16_t*)m->scales + (size_t)r * ng;
-      for (int j = 0; j < K; ++j)
+      int j = 0;
+#ifdef ORACLE_AVX2
+      /* 8 columns at a time: sign-extend nibbles, times the group scale */
+      for (; j + 8 <= K; j += 8) {
+        const uint32_t b4 = (uint32_t)row[j / 2] | ((uint32_t)row[j / 2 + 1] << 8) |
+                            ((uint32_t)row[j / 2 + 2] << 16) | ((uint32_t)row[j / 2 + 3] << 24);
+        const __m256i sh = _mm256_setr_epi32(28, 24, 20, 16, 12, 8, 4, 0);
+        const __m256i q = _mm256_srai_epi32(_mm256_sllv_epi32(_mm256_set1_epi32((int)b4), sh), 28);
+        const __m256 s = _mm256_set1_ps(oracle_fp16_to_fp32(gs[j / 32]));
+        _mm256_storeu_ps(dst + j, _mm256_mul_ps(_mm256_cvtepi32_ps(q), s));
+      }
+#endif
+      for (; j < K; ++j)
         dst[j] = (float)oracle_int4_nibble(row[j / 2], j & 1) * oracle_fp16_to_fp32(gs[j / 32]);
       break;
     }
