@@ -20,7 +20,6 @@ namespace cpi {
 
 constexpr int kAttnBlock = 256;
 constexpr int kAttnWaves = kAttnBlock / kWave;
-constexpr int kSubTile = 64;  // tokens per online-softmax step
 
 struct AttnParams {
   const void* q;
@@ -35,200 +34,250 @@ struct AttnParams {
   float* scratch;       // [nh][MAXS][2] m,l  then [nh][MAXS][hd] o
 };
 
-__device__ __forceinline__ void attn_range(const AttnParams& p, int split, int& t0, int& t1,
-                                           int& active) {
+// Scratch layout (floats): [0, 64) reserved, then m,l [nh][MAXS][2], then
+// o [nh][MAXS][hd].
+constexpr int kCounterSlots = 64;
+
+__device__ __forceinline__ float safe_exp_diff(float a, float m) {
+  return (a == -INFINITY) ? 0.f : expf(a - m);
+}
+
+template <int HD, int G, bool QF32, bool OF32>
+__global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
+  constexpr int LPK = HD / 8;               // lanes per K/V row: 16 B each
+  constexpr int NG = kAttnBlock / LPK;      // token groups per workgroup
+  constexpr int GPW = kWave / LPK;          // token groups per wave
+  constexpr int TB = 2;                     // tokens per group per iteration
+  constexpr int CT = NG * TB;               // tokens per workgroup iteration
+
+  __shared__ float wm[kAttnWaves][G], wl[kAttnWaves][G];
+  __shared__ float wo[kAttnWaves][G][HD];
+  
+  const int kvh = blockIdx.x;
+  const int split = blockIdx.y;
   int seq = p.position ? (*p.position + 1) : p.seq_len;
   if (seq > p.max_ctx) seq = p.max_ctx;
   const int start = (p.window > 0 && seq > p.window) ? seq - p.window : 0;
   const int len = seq - start;
   int chunk = (len + p.nsplit - 1) / p.nsplit;
-  chunk = ((chunk + 15) / 16) * 16;
-  if (chunk < 16) chunk = 16;
-  active = (len + chunk - 1) / chunk;
-  t0 = start + split * chunk;
-  t1 = t0 + chunk;
-  if (t1 > seq) t1 = seq;
-}
+  chunk = ((chunk + CT - 1) / CT) * CT;
+  if (chunk < CT) chunk = CT;
+  const int active = (len + chunk - 1) / chunk;
+  if (split >= active) return;  // uniform per workgroup
+  const int t0 = start + split * chunk;
+  const int t1 = min(t0 + chunk, seq);
 
-template <int HD, int G, bool QF32>
-__global__ void __launch_bounds__(kAttnBlock) attn_partial_kernel(AttnParams p) {
-  constexpr int LPK = HD / 8;                 // lanes per key row (16 B each)
-  constexpr int KPP = kAttnBlock / LPK;       // keys per pass
-  constexpr int CB = HD / 8;                  // 16-byte column blocks of V
-  constexpr int TSUB = kAttnBlock / CB;       // token subsets in the V phase
-  constexpr int TSUB_W = kWave / CB;          // token subsets inside one wave
-  static_assert(kSubTile % KPP == 0 || KPP % kSubTile == 0, "tile");
-
-  __shared__ float q_s[G][HD];
-  __shared__ float s_s[G][kSubTile];
-  __shared__ float alpha_s[G];
-  __shared__ float red_s[kAttnWaves][G][HD];
-
-  const int kvh = blockIdx.x;
-  const int split = blockIdx.y;
-  int t0, t1, active;
-  attn_range(p, split, t0, t1, active);
-  if (split >= active) return;  // uniform per block
-
-  const int kvdim = p.nkv * HD;
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
   const int wave = tid / kWave;
+  const int cb = tid % LPK;
+  const int gid = tid / LPK;
+  const int kvdim = p.nkv * HD;
+  const size_t col = static_cast<size_t>(kvh) * HD + cb * 8;
 
-  for (int i = tid; i < G * HD; i += kAttnBlock) {
-    const int g = i / HD, d = i % HD;
-    const int qi = (kvh * G + g) * HD + d;
-    q_s[g][d] = QF32 ? static_cast<const float*>(p.q)[qi]
-                     : h2f(static_cast<const uint16_t*>(p.q)[qi]);
-  }
-  __syncthreads();
-
-  // Running softmax state (m, l) per head lives in shared memory and is
-  // owned by the wave that handles that head in the softmax step.
-  __shared__ float m_s[G], l_s[G];
-  if (tid < G) { m_s[tid] = -INFINITY; l_s[tid] = 0.f; }
-  // V accumulators: this thread owns column block cb and token subset ts.
-  const int cb = tid % CB;
-  const int ts = tid / CB;
-  float o[G][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
-  __syncthreads();
-
-  for (int base = t0; base < t1; base += kSubTile) {
-    const int n = min(kSubTile, t1 - base);
-    // ---- scores for up to 64 tokens
-    const int kpart = tid % LPK;
-    for (int kk = tid / LPK; kk < kSubTile; kk += KPP) {
-      float dots[G];
-#pragma unroll
-      for (int g = 0; g < G; ++g) dots[g] = 0.f;
-      if (kk < n) {
-        const uint4 kw = *reinterpret_cast<const uint4*>(
-            p.k + static_cast<size_t>(base + kk) * kvdim + kvh * HD + kpart * 8);
-        const uint32_t kd[4] = {kw.x, kw.y, kw.z, kw.w};
-        float kf[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const f16x2 h = as_h2(kd[e]);
-          kf[2 * e] = static_cast<float>(h.x);
-          kf[2 * e + 1] = static_cast<float>(h.y);
-        }
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dots[g] = fmaf(q_s[g][kpart * 8 + e], kf[e], dots[g]);
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float d = group_sum<LPK>(dots[g]);
-        if (kpart == 0) s_s[g][kk] = (kk < n) ? d * p.scale : -INFINITY;
-      }
-    }
-    __syncthreads();
-    // ---- online softmax update: wave w handles heads w, w+4, ...
-    for (int g = wave; g < G; g += kAttnWaves) {
-      const float sv = s_s[g][lane];
-      const float m_old = m_s[g];
-      const float m_new = fmaxf(m_old, wave_max(sv));
-      const float pv = (lane < n) ? expf(sv - m_new) : 0.f;
-      const float psum = wave_sum(pv);
-      s_s[g][lane] = pv;
-      if (lane == 0) {
-        const float a = expf(m_old - m_new);  // 0 on the first tile
-        alpha_s[g] = a;
-        l_s[g] = l_s[g] * a + psum;
-        m_s[g] = m_new;
-      }
-    }
-    __syncthreads();
-    // ---- rescale and accumulate V
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float a = alpha_s[g];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] *= a;
-    }
-    for (int tt = ts; tt < n; tt += TSUB) {
-      const uint4 vw = *reinterpret_cast<const uint4*>(
-          p.v + static_cast<size_t>(base + tt) * kvdim + kvh * HD + cb * 8);
-      const uint32_t vd[4] = {vw.x, vw.y, vw.z, vw.w};
-      float vf[8];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const f16x2 h = as_h2(vd[e]);
-        vf[2 * e] = static_cast<float>(h.x);
-        vf[2 * e + 1] = static_cast<float>(h.y);
-      }
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float pw = s_s[g][tt];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[g][e] = fmaf(pw, vf[e], o[g][e]);
-      }
-    }
-    __syncthreads();  // s_s / alpha_s are rewritten by the next tile
-  }
-
-  // ---- reduce the token subsets: inside the wave, then across waves
+  float qv[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float v = o[g][e];
+      const int qi = (kvh * G + g) * HD + cb * 8 + e;
+      const float v = QF32 ? static_cast<const float*>(p.q)[qi] : h2f(static_cast<const uint16_t*>(p.q)[qi]);
+      qv[g][e] = v * p.scale;
+    }
+  float m[G], l[G], o[G][8];
 #pragma unroll
-      for (int m = CB; m < kWave; m <<= 1) v += __shfl_xor(v, m, kWave);
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+  }
+
+  for (int base = t0 + gid * TB; base < t1; base += CT) {
+    float kf[TB][8], vf[TB][8];
+    bool valid[TB];
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int t = base + tb;
+      valid[tb] = t < t1;
+      const size_t row = static_cast<size_t>(valid[tb] ? t : t1 - 1) * kvdim + col;
+      const u32x4 kw = *reinterpret_cast<const u32x4*>(p.k + row);
+      const u32x4 vw = *reinterpret_cast<const u32x4*>(p.v + row);
+      const uint32_t kd[4] = {kw.x, kw.y, kw.z, kw.w};
+      const uint32_t vd[4] = {vw.x, vw.y, vw.z, vw.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const f16x2 kh = as_h2(kd[e]);
+        const f16x2 vh = as_h2(vd[e]);
+        kf[tb][2 * e] = static_cast<float>(kh.x);
+        kf[tb][2 * e + 1] = static_cast<float>(kh.y);
+        vf[tb][2 * e] = static_cast<float>(vh.x);
+        vf[tb][2 * e + 1] = static_cast<float>(vh.y);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float sc[TB];
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[tb][e], d);
+        d = group_sum<LPK>(d);
+        sc[tb] = valid[tb] ? d : -INFINITY;
+      }
+      float mx = sc[0];
+#pragma unroll
+      for (int tb = 1; tb < TB; ++tb) mx = fmaxf(mx, sc[tb]);
+      const float m_new = fmaxf(m[g], mx);
+      if (m_new == -INFINITY) continue;  // no token seen yet by this group
+      const float a = safe_exp_diff(m[g], m_new);
+      float pw[TB];
+      float ps = 0.f;
+#pragma unroll
+      for (int tb = 0; tb < TB; ++tb) {
+        pw[tb] = safe_exp_diff(sc[tb], m_new);
+        ps += pw[tb];
+      }
+      l[g] = l[g] * a + ps;
+      m[g] = m_new;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float acc = o[g][e] * a;
+#pragma unroll
+        for (int tb = 0; tb < TB; ++tb) acc = fmaf(pw[tb], vf[tb][e], acc);
+        o[g][e] = acc;
+      }
+    }
+  }
+
+  // ---- merge the token groups of this wave (shuffles over the group bits)
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float M = m[g];
+#pragma unroll
+    for (int off = LPK; off < kWave; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, kWave));
+    const float sc = (M == -INFINITY) ? 0.f : safe_exp_diff(m[g], M);
+    float lv = l[g] * sc;
+#pragma unroll
+    for (int off = LPK; off < kWave; off <<= 1) lv += __shfl_xor(lv, off, kWave);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = o[g][e] * sc;
+#pragma unroll
+      for (int off = LPK; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
       o[g][e] = v;
     }
-  if (lane < CB) {
+    if (lane < LPK) {
 #pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) red_s[wave][g][cb * 8 + e] = o[g][e];
+      for (int e = 0; e < 8; ++e) wo[wave][g][cb * 8 + e] = o[g][e];
+      if (lane == 0) {
+        wm[wave][g] = M;
+        wl[wave][g] = lv;
+      }
+    }
   }
+  (void)GPW;
   __syncthreads();
+
+  // ---- merge the waves; either finish (single split) or publish a partial
   const size_t maxs = CPI_ATTN_MAX_SPLITS;
-  float* ml = p.scratch;
-  float* os = p.scratch + static_cast<size_t>(p.nh) * maxs * 2;
+  float* ml = p.scratch + kCounterSlots;
+  float* os = ml + static_cast<size_t>(p.nh) * maxs * 2;
   for (int i = tid; i < G * HD; i += kAttnBlock) {
     const int g = i / HD, d = i % HD;
-    float v = 0.f;
+    float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) v += red_s[w][g][d];
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][g]);
+    float L = 0.f, acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float sc = safe_exp_diff(wm[w][g], M);
+      L = fmaf(wl[w][g], sc, L);
+      acc = fmaf(wo[w][g][d], sc, acc);
+    }
     const int h = kvh * G + g;
-    os[(static_cast<size_t>(h) * maxs + split) * HD + d] = v;
-  }
-  if (tid < G) {
-    const int h = kvh * G + tid;
-    ml[(static_cast<size_t>(h) * maxs + split) * 2 + 0] = m_s[tid];
-    ml[(static_cast<size_t>(h) * maxs + split) * 2 + 1] = l_s[tid];
+    if (active == 1) {
+      const float r = acc / L;
+      if (OF32) static_cast<float*>(p.out)[h * HD + d] = r;
+      else static_cast<uint16_t*>(p.out)[h * HD + d] = f2h(r);
+    } else {
+      os[(static_cast<size_t>(h) * maxs + split) * HD + d] = acc;
+      if (d == 0) {
+        ml[(static_cast<size_t>(h) * maxs + split) * 2 + 0] = M;
+        ml[(static_cast<size_t>(h) * maxs + split) * 2 + 1] = L;
+      }
+    }
   }
 }
 
-// Merge the split partials of one query head:  M = max m_s,
-// L = sum l_s e^(m_s - M),  out = sum o_s e^(m_s - M) / L   (fixed order).
+// Merge the split partials of one query head (fixed order):
+//   M = max m_s,  L = sum l_s e^(m_s - M),  out = sum o_s e^(m_s - M) / L.
+// One workgroup per head; the split axis is spread over the threads so the
+// loads are independent.
 template <int HD, bool OF32>
-__global__ void __launch_bounds__(HD) attn_merge_kernel(AttnParams p) {
+__global__ void __launch_bounds__(kAttnBlock) attn_merge_kernel(AttnParams p) {
+  constexpr int SUB = kAttnBlock / HD * 4;  // split lanes per column (4 columns per thread)
+  __shared__ float wsh[CPI_ATTN_MAX_SPLITS];
+  __shared__ float red[kAttnWaves];
+  __shared__ float part[SUB][HD];
   const int h = blockIdx.x;
-  const int d = threadIdx.x;
-  int t0, t1, active;
-  attn_range(p, 0, t0, t1, active);
+  int seq = p.position ? (*p.position + 1) : p.seq_len;
+  if (seq > p.max_ctx) seq = p.max_ctx;
+  const int start = (p.window > 0 && seq > p.window) ? seq - p.window : 0;
+  const int len = seq - start;
+  constexpr int CT = (kAttnBlock / (HD / 8)) * 2;
+  int chunk = (len + p.nsplit - 1) / p.nsplit;
+  chunk = ((chunk + CT - 1) / CT) * CT;
+  if (chunk < CT) chunk = CT;
+  const int active = (len + chunk - 1) / chunk;
+  if (active <= 1) return;  // the split kernel already wrote the output
   const size_t maxs = CPI_ATTN_MAX_SPLITS;
-  const float* ml = p.scratch + static_cast<size_t>(h) * maxs * 2;
-  const float* os = p.scratch + static_cast<size_t>(p.nh) * maxs * 2 + static_cast<size_t>(h) * maxs * HD;
-  float M = -INFINITY;
-  for (int s = 0; s < active; ++s) M = fmaxf(M, ml[2 * s]);
-  float L = 0.f, acc = 0.f;
-  for (int s = 0; s < active; ++s) {
-    const float w = expf(ml[2 * s] - M);
-    L = fmaf(ml[2 * s + 1], w, L);
-    acc = fmaf(os[static_cast<size_t>(s) * HD + d], w, acc);
+  const float* ml = p.scratch + kCounterSlots + static_cast<size_t>(h) * maxs * 2;
+  const float* os = p.scratch + kCounterSlots + static_cast<size_t>(p.nh) * maxs * 2 +
+                    static_cast<size_t>(h) * maxs * HD;
+  const int tid = threadIdx.x;
+  float mv = -INFINITY;
+  if (tid < active) mv = ml[2 * tid];
+  // block max of m
+  float M = wave_max(mv);
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = M;
+  __syncthreads();
+  M = red[0];
+#pragma unroll
+  for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red[w]);
+  __syncthreads();
+  float lw = 0.f;
+  if (tid < active) {
+    const float w = safe_exp_diff(mv, M);
+    wsh[tid] = w;
+    lw = ml[2 * tid + 1] * w;
   }
-  const float r = (active > 0) ? acc / L : 0.f;
-  if (OF32) static_cast<float*>(p.out)[h * HD + d] = r;
-  else static_cast<uint16_t*>(p.out)[h * HD + d] = f2h(r);
+  const float L = block_sum(lw, red);  // includes a barrier: wsh is visible
+  // columns: thread handles 4 consecutive columns for splits s = sub, sub+SUB, ...
+  const int c4 = (tid % (HD / 4)) * 4;
+  const int sub = tid / (HD / 4);
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int s2 = sub; s2 < active; s2 += SUB) {
+    const float w = wsh[s2];
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 v = *reinterpret_cast<const f32x4*>(os + static_cast<size_t>(s2) * HD + c4);
+    acc[0] = fmaf(v.x, w, acc[0]);
+    acc[1] = fmaf(v.y, w, acc[1]);
+    acc[2] = fmaf(v.z, w, acc[2]);
+    acc[3] = fmaf(v.w, w, acc[3]);
+  }
+#pragma unroll
+  for (int e = 0; e < 4; ++e) part[sub][c4 + e] = acc[e];
+  __syncthreads();
+  if (tid < HD) {
+    float r = 0.f;
+#pragma unroll
+    for (int q = 0; q < SUB; ++q) r += part[q][tid];
+    r /= L;
+    if (OF32) static_cast<float*>(p.out)[h * HD + tid] = r;
+    else static_cast<uint16_t*>(p.out)[h * HD + tid] = f2h(r);
+  }
 }
 
 namespace {
@@ -236,12 +285,14 @@ namespace {
 template <int HD, int G>
 hipError_t launch_g(const AttnParams& p, bool qf32, bool of32, hipStream_t s) {
   dim3 grid(p.nkv, p.nsplit);
-  if (qf32) hipLaunchKernelGGL((attn_partial_kernel<HD, G, true>), grid, dim3(kAttnBlock), 0, s, p);
-  else hipLaunchKernelGGL((attn_partial_kernel<HD, G, false>), grid, dim3(kAttnBlock), 0, s, p);
+  if (qf32 && of32) hipLaunchKernelGGL((attn_kernel<HD, G, true, true>), grid, dim3(kAttnBlock), 0, s, p);
+  else if (qf32) hipLaunchKernelGGL((attn_kernel<HD, G, true, false>), grid, dim3(kAttnBlock), 0, s, p);
+  else if (of32) hipLaunchKernelGGL((attn_kernel<HD, G, false, true>), grid, dim3(kAttnBlock), 0, s, p);
+  else hipLaunchKernelGGL((attn_kernel<HD, G, false, false>), grid, dim3(kAttnBlock), 0, s, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (of32) hipLaunchKernelGGL((attn_merge_kernel<HD, true>), dim3(p.nh), dim3(HD), 0, s, p);
-  else hipLaunchKernelGGL((attn_merge_kernel<HD, false>), dim3(p.nh), dim3(HD), 0, s, p);
+  if (of32) hipLaunchKernelGGL((attn_merge_kernel<HD, true>), dim3(p.nh), dim3(kAttnBlock), 0, s, p);
+  else hipLaunchKernelGGL((attn_merge_kernel<HD, false>), dim3(p.nh), dim3(kAttnBlock), 0, s, p);
   return hipGetLastError();
 }
 
@@ -261,7 +312,7 @@ hipError_t launch_hd(const AttnParams& p, int G, bool qf32, bool of32, hipStream
 // Split count: enough workgroups to cover the 256 CUs several times at long
 // context, bounded by the scratch capacity.
 int attn_num_splits(int nkv) {
-  int n = 1024 / (nkv > 0 ? nkv : 1);
+  int n = 512 / (nkv > 0 ? nkv : 1);
   if (n < 1) n = 1;
   if (n > CPI_ATTN_MAX_SPLITS) n = CPI_ATTN_MAX_SPLITS;
   return n;

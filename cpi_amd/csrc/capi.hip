@@ -200,7 +200,7 @@ int cpi_hip_gather_rows(const void* src, void* dst, const int* idx, int rows, si
 
 // ------------------------------------------------------------ attention
 size_t cpi_hip_attention_scratch_floats(int nh, int hd) {
-  return static_cast<size_t>(nh) * CPI_ATTN_MAX_SPLITS * (hd + 2);
+  return 64 + static_cast<size_t>(nh) * CPI_ATTN_MAX_SPLITS * (hd + 2);
 }
 
 int cpi_hip_attention_decode(const void* q, int q_is_f32, const uint16_t* k, const uint16_t* v,
@@ -210,6 +210,7 @@ int cpi_hip_attention_decode(const void* q, int q_is_f32, const uint16_t* k, con
   if (!q || !k || !v || !out || !scratch) return fail("attention_decode: null pointer");
   if (!cpi::attn_supported(nh, nkv, hd))
     return fail("attention_decode: supported shapes are head_dim 64/128 and nh/nkv in {1,2,4,8}");
+  if (nkv > 64) return fail("attention_decode: at most 64 KV heads");
   if (!position && (seq_len <= 0 || seq_len > max_ctx))
     return fail("attention_decode: seq_len must be in [1, max_context]");
   return check(cpi::attn_launch(q, q_is_f32 != 0, k, v, out, out_is_f32 != 0, seq_len, position,

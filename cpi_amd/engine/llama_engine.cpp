@@ -287,6 +287,7 @@ void LlamaEngine::initialize(const EngineOptions& options) {
   ff_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(I) * 4));
   logits_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(V) * 4));
   attn_scratch_ = static_cast<float*>(dmalloc(cpi_hip_attention_scratch_floats(NH, head_dim_) * 4));
+  HIP_OK(hipMemset(attn_scratch_, 0, cpi_hip_attention_scratch_floats(NH, head_dim_) * 4));
   d_token_ = static_cast<int*>(dmalloc(4));
   d_pos_ = static_cast<int*>(dmalloc(4));
   d_step_ = static_cast<int*>(dmalloc(4));

@@ -103,7 +103,7 @@ def time_attention(nh, nkv, hd, ctx, iters=100, rotate_bytes=2 << 30):
                torch.randn(ctx * nkv * hd, device="cuda", generator=gen).half()) for _ in range(copies)]
     q = torch.randn(nh * hd, device="cuda", generator=gen)
     out = torch.empty(nh * hd, device="cuda")
-    scratch = torch.empty(_lib.lib().cpi_hip_attention_scratch_floats(nh, hd), device="cuda")
+    scratch = torch.zeros(_lib.lib().cpi_hip_attention_scratch_floats(nh, hd), device="cuda")
     fn = _lib.lib().cpi_hip_attention_decode
 
     def launch_all(n):

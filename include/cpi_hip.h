@@ -153,7 +153,8 @@ int cpi_hip_gather_rows(const void* src, void* dst, const int* idx, int rows,
  * Decode attention (exact online softmax, split-K over context, GQA).
  * q fp32 or fp16 [num_heads*head_dim] (q_is_f32), caches fp16
  * [max_ctx, num_kv_heads*head_dim], out fp32 or fp16 [num_heads*head_dim].
- * Scratch: fp32 [num_heads * CPI_ATTN_MAX_SPLITS * (head_dim + 2)].
+ * Scratch: cpi_hip_attention_scratch_floats() floats (split partials);
+ * calls sharing one scratch buffer must not overlap.
  * Replaces launch_attention_step / _device_pos (kernels.cuh:216-275):
  * chunk_stats + chunk_reduce, gqa_decode_kernel and the tiled kernel.
  * ---------------------------------------------------------------------- */
