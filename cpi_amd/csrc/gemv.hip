@@ -26,15 +26,13 @@
 #include <cstdlib>
 
 #include "common.hpp"
+#include "gemv_plan.hpp"
 #include "../../include/cpi_hip.h"
 
 namespace cpi {
 
-constexpr int kChunkCols = 8;                 // 16-byte chunks per row per step
-constexpr int kTileRows = kWave / kChunkCols; // rows per wave tile
-constexpr int kWavesPerBlock = 4;
 constexpr int kBlock = kWave * kWavesPerBlock;
-constexpr int kUnroll = 8;
+static_assert(kTileRows * kChunkCols == kWave, "a wave covers 8 rows x 8 chunks");
 
 template <int FMT> struct FmtT;
 template <> struct FmtT<CPI_W_F16> {
@@ -72,6 +70,14 @@ struct GemvParams {
 };
 
 enum { EPI_DUAL_F16 = 100 };
+
+// Workgroup barrier that only orders LDS: waits for this wave's LDS operations
+// (lgkmcnt) but leaves outstanding global loads in flight, unlike
+// __syncthreads(), whose fence drains them.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // vmcnt=63 (no wait), expcnt=7, lgkmcnt=0
+  __builtin_amdgcn_s_barrier();
+}
 
 // ---------------------------------------------------------------------------
 // Activation preparation (one chunk).
@@ -141,24 +147,21 @@ __device__ __forceinline__ float chunk_dot(const u32x4 w, const uint32_t* p, flo
     const uint4 pl = *reinterpret_cast<const uint4*>(p + 4);
     const uint32_t h[4] = {ph.x, ph.y, ph.z, ph.w};
     const uint32_t l[4] = {pl.x, pl.y, pl.z, pl.w};
+    float t[4];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      acc = dot2(wd[d], h[d], acc);
-      acc = dot2(wd[d], l[d], acc);
-    }
-    return acc;
+    for (int d = 0; d < 4; ++d) t[d] = dot2(wd[d], l[d], dot2(wd[d], h[d], 0.f));
+    return acc + ((t[0] + t[1]) + (t[2] + t[3]));
   } else if constexpr (FMT == CPI_W_I8ROW) {
     // (w ^ 0x80808080) & 0x00FF00FF | 0x64006400 == (w & 0x00FF00FF) ^ 0x64806480
     const uint4 a = *reinterpret_cast<const uint4*>(p);
     const uint4 b = *reinterpret_cast<const uint4*>(p + 4);
     const uint32_t pp[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    float t0 = __builtin_bit_cast(float, p[8]), t1 = 0.f;
+    float t[4];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      t0 = dot2((wd[d] & 0x00FF00FFu) ^ 0x64806480u, pp[2 * d], t0);
-      t1 = dot2(((wd[d] >> 8) & 0x00FF00FFu) ^ 0x64806480u, pp[2 * d + 1], t1);
-    }
-    return acc + (t0 + t1);
+    for (int d = 0; d < 4; ++d)
+      t[d] = dot2(((wd[d] >> 8) & 0x00FF00FFu) ^ 0x64806480u, pp[2 * d + 1],
+                  dot2((wd[d] & 0x00FF00FFu) ^ 0x64806480u, pp[2 * d], 0.f));
+    return acc + (((t[0] + t[1]) + (t[2] + t[3])) + __builtin_bit_cast(float, p[8]));
   } else {
     // Two's complement nibble n -> offset binary n ^ 8, placed under the
     // exponent of 1024.0:  (w & M) ^ (0x6400 | 8<<shift) per half.
@@ -171,17 +174,19 @@ __device__ __forceinline__ float chunk_dot(const u32x4 w, const uint32_t* p, flo
       pp[4 * i + 2] = a.z;
       pp[4 * i + 3] = a.w;
     }
-    float t0 = __builtin_bit_cast(float, p[16]), t1 = 0.f;
+    // four independent dot chains (one per weight dword) keep v_dot2 latency
+    // off the critical path
+    float t[4];
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
       const uint32_t u = wd[d];
       const uint32_t u8 = u >> 8;
-      t0 = dot2((u & 0x000F000Fu) ^ 0x64086408u, pp[4 * d + 0], t0);
-      t1 = dot2((u & 0x00F000F0u) ^ 0x64806480u, pp[4 * d + 1], t1);
-      t0 = dot2((u8 & 0x000F000Fu) ^ 0x64086408u, pp[4 * d + 2], t0);
-      t1 = dot2((u8 & 0x00F000F0u) ^ 0x64806480u, pp[4 * d + 3], t1);
+      float a = dot2((u & 0x000F000Fu) ^ 0x64086408u, pp[4 * d + 0], 0.f);
+      a = dot2((u & 0x00F000F0u) ^ 0x64806480u, pp[4 * d + 1], a);
+      a = dot2((u8 & 0x000F000Fu) ^ 0x64086408u, pp[4 * d + 2], a);
+      t[d] = dot2((u8 & 0x00F000F0u) ^ 0x64806480u, pp[4 * d + 3], a);
     }
-    return t0 + t1;  // caller applies the group scale / accumulates
+    return ((t[0] + t[1]) + (t[2] + t[3])) + __builtin_bit_cast(float, p[16]);  // caller scales
   }
 }
 
@@ -215,68 +220,43 @@ __device__ __forceinline__ float load_x(const void* x, int i) {
 // ---------------------------------------------------------------------------
 // Kernel pieces.
 // ---------------------------------------------------------------------------
-struct TileCtx {
-  const uint8_t* wrow;   // this lane's weight row
-  const uint16_t* grow;  // this lane's group-scale row (I4G32)
-  int row;
-  bool row_ok;
+// One pipeline slot: kUnroll weight chunks (and their raw fp16 group scales)
+// of one lane.
+struct Slot {
+  u32x4 w[kUnroll];
+  uint32_t g[kUnroll];
 };
 
 template <int FMT>
-__device__ __forceinline__ TileCtx tile_ctx(const GemvParams& p, int t, int r, int nchunks,
-                                            size_t row_bytes) {
-  TileCtx c;
-  c.row = t * kTileRows + r;
-  c.row_ok = c.row < p.R;
-  const int rowc = c.row_ok ? c.row : (p.R - 1);
-  c.wrow = static_cast<const uint8_t*>(p.w) + static_cast<size_t>(rowc) * row_bytes;
-  c.grow = nullptr;
-  if constexpr (FMT == CPI_W_I4G32)
-    c.grow = static_cast<const uint16_t*>(p.scales) + static_cast<size_t>(rowc) * nchunks;
-  return c;
-}
-
-// Issue the weight (and group-scale) loads of batch b of a tile.
-template <int FMT>
-__device__ __forceinline__ void load_batch(const TileCtx& tc, int b, int j, int nchunks,
-                                           u32x4 (&w)[kUnroll], float (&g)[kUnroll]) {
+__device__ __forceinline__ void load_slot(const GemvGeom& g, const BatchPos& bp, const uint8_t* W,
+                                          const uint16_t* G, int r, int j, Slot& s) {
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int c = (b * kUnroll + u) * kChunkCols + j;
-    const int cc = c < nchunks ? c : nchunks - 1;  // clamped: always a valid address
-    w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tc.wrow) + cc);
-    if constexpr (FMT == CPI_W_I4G32) g[u] = h2f(tc.grow[cc]);
+    s.w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W + weight_offset(g, bp, r, j, u)));
+    if constexpr (FMT == CPI_W_I4G32) s.g[u] = G[scale_index(g, bp, r, j, u)];
   }
 }
 
 template <int FMT>
-__device__ __forceinline__ float compute_batch(const uint32_t* lds, int b, int j, int nchunks,
-                                               const u32x4 (&w)[kUnroll], const float (&g)[kUnroll],
-                                               float acc) {
+__device__ __forceinline__ float compute_slot(const uint32_t* lds_lane, const GemvGeom& g,
+                                              const BatchPos& bp, int j, const Slot& s, float acc) {
   using F = FmtT<FMT>;
-  if ((b * kUnroll + kUnroll) * kChunkCols <= nchunks) {  // full batch: no predication
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      const int c = (b * kUnroll + u) * kChunkCols + j;
-      const uint32_t* pc = lds + c * F::kStride;
-      if constexpr (FMT == CPI_W_I4G32) acc = fmaf(g[u], chunk_dot<FMT>(w[u], pc, 0.f), acc);
-      else if constexpr (FMT == CPI_W_I4ROW) acc += chunk_dot<FMT>(w[u], pc, 0.f);
-      else acc = chunk_dot<FMT>(w[u], pc, acc);
-    }
-    return acc;
-  }
+  const uint32_t* pb = lds_lane + bp.cbase * F::kStride;
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
-    const int c = (b * kUnroll + u) * kChunkCols + j;
-    if (c < nchunks) {
-      const uint32_t* pc = lds + c * F::kStride;
-      if constexpr (FMT == CPI_W_I4G32) acc = fmaf(g[u], chunk_dot<FMT>(w[u], pc, 0.f), acc);
-      else if constexpr (FMT == CPI_W_I4ROW) acc += chunk_dot<FMT>(w[u], pc, 0.f);
-      else acc = chunk_dot<FMT>(w[u], pc, acc);
-    }
+    if (!bp.full && bp.cbase + u * kChunkCols + j >= g.nchunks) continue;  // past the row end
+    const uint32_t* pc = pb + u * kChunkCols * F::kStride;
+    if constexpr (FMT == CPI_W_I4G32) acc = fmaf(h2f(static_cast<uint16_t>(s.g[u])), chunk_dot<FMT>(s.w[u], pc, 0.f), acc);
+    else if constexpr (FMT == CPI_W_I4ROW) acc += chunk_dot<FMT>(s.w[u], pc, 0.f);
+    else acc = chunk_dot<FMT>(s.w[u], pc, acc);
   }
   return acc;
 }
+
+struct TileCtx {
+  int row;
+  bool row_ok;
+};
 
 // Reduce the 8 chunk-column partials of each row and run the epilogue.
 template <int FMT, int EPI>
@@ -351,9 +331,8 @@ __device__ __forceinline__ void finish_tile(const GemvParams& p, int t, int r, i
 // Kernel.  A workgroup's 4 waves cover TPW = 4/KS tiles per iteration, each
 // tile split into KS K-segments (one wave each, equal batch counts, reduced
 // through LDS in a fixed order).  Each wave walks its work as a flat sequence
-// of load batches with two register buffers: the loads of batch i+1 are in
-// flight while batch i is computed, and the first batch is issued before the
-// activation prologue so HBM latency overlaps the preparation.
+// of batches through a ring of three register slots (prefetch distance two);
+// the first two batches are issued before the activation prologue.
 // ---------------------------------------------------------------------------
 template <int FMT, int EPI, bool XF32>
 __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int ks) {
@@ -363,82 +342,153 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int ks) {
   __shared__ float part[kWavesPerBlock][kTileRows];
 
   const int K = p.K;
-  const int nchunks = K / F::kElems;
+  const GemvGeom geo = make_geom(p.R, K, F::kElems, ks, gridDim.x);
+  const int nchunks = geo.nchunks;
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int r = lane / kChunkCols;
   const int j = lane % kChunkCols;
-  const int tpw = kWavesPerBlock / ks;      // tiles per workgroup iteration
+  const int tpw = geo.tpw;
   const int seg = wave % ks;
-  const int tiles = (p.R + kTileRows - 1) / kTileRows;
-  const int steps = (nchunks + kChunkCols - 1) / kChunkCols;
-  const int nbt = (steps + kUnroll - 1) / kUnroll;  // batches per tile
-  const int nbs = (nbt + ks - 1) / ks;               // batches per segment
-  const int b0 = seg * nbs;
-  const size_t row_bytes = static_cast<size_t>(K) * 16 / F::kElems;
-  const int groups = (tiles + tpw - 1) / tpw;
+  const int tiles = geo.tiles;
+  const int nbs = geo.nbs;
+  const int wtile = wave / ks;
+  const uint8_t* W = static_cast<const uint8_t*>(p.w);
+  const uint16_t* G = static_cast<const uint16_t*>(p.scales);
+  const int total = my_groups(geo, blockIdx.x) * nbs;
+  auto addr_of = [&](int g, int bb) { return batch_pos(geo, blockIdx.x, wave, g, bb); };
 
-  int gi = blockIdx.x;                       // tile-group index of this workgroup
-  int t = gi * tpw + wave / ks;
-  int b = 0;                                 // batch index within the segment
-  TileCtx tc = tile_ctx<FMT>(p, t < tiles ? t : 0, r, nchunks, row_bytes);
-  u32x4 wa[kUnroll], wb[kUnroll];
-  float ga[kUnroll], gb[kUnroll];
-  if (gi < groups && t < tiles) load_batch<FMT>(tc, b0, j, nchunks, wa, ga);
-
-  // ---- prologue: optional RMSNorm statistics, then activation preparation
-  float inv_rms = 1.f;
-  if (p.norm_w != nullptr) {
-    float ss = 0.f;
-    for (int c = threadIdx.x; c < K / 8; c += kBlock) {
-      float v[8];
-      load_x8<XF32>(p.x, c, v);
+  // ---- prologue part 1: activations (and norm weights) into registers
+  constexpr int MAXC = 64 / F::kElems;  // chunks per thread held in registers
+  const bool in_regs = nchunks <= MAXC * kBlock;
+  float xr[MAXC][F::kElems];
+  uint32_t nr[MAXC][F::kElems / 2];
+  if (in_regs) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
-    }
-    ss = block_sum(ss, red);
-    inv_rms = 1.f / sqrtf(ss / static_cast<float>(K) + p.eps);
-  }
-  for (int c = threadIdx.x; c < nchunks; c += kBlock) {
-    float v[F::kElems];
+    for (int q = 0; q < MAXC; ++q) {
+      const int c = threadIdx.x + q * kBlock;
+      if (c < nchunks) {
 #pragma unroll
-    for (int e8 = 0; e8 < F::kElems / 8; ++e8) {
-      load_x8<XF32>(p.x, c * (F::kElems / 8) + e8, v + 8 * e8);
-      if (p.norm_w != nullptr) {
-        const u32x4 nw = *reinterpret_cast<const u32x4*>(p.norm_w + (c * (F::kElems / 8) + e8) * 8);
-        const uint32_t nd[4] = {nw.x, nw.y, nw.z, nw.w};
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const f16x2 h = as_h2(nd[q]);
-          v[8 * e8 + 2 * q] = (inv_rms * v[8 * e8 + 2 * q]) * static_cast<float>(h.x);
-          v[8 * e8 + 2 * q + 1] = (inv_rms * v[8 * e8 + 2 * q + 1]) * static_cast<float>(h.y);
+        for (int e8 = 0; e8 < F::kElems / 8; ++e8) {
+          load_x8<XF32>(p.x, c * (F::kElems / 8) + e8, &xr[q][8 * e8]);
+          if (p.norm_w != nullptr) {
+            const u32x4 nw = *reinterpret_cast<const u32x4*>(p.norm_w + (c * (F::kElems / 8) + e8) * 8);
+            nr[q][4 * e8 + 0] = nw.x; nr[q][4 * e8 + 1] = nw.y;
+            nr[q][4 * e8 + 2] = nw.z; nr[q][4 * e8 + 3] = nw.w;
+          }
         }
       }
     }
-    prep_chunk<FMT>(v, lds + c * F::kStride);
   }
-  __syncthreads();
 
+  // ---- first two batches in flight before the activations are consumed
+  int gi = blockIdx.x, b = 0;
+  int g1 = gi, b1 = 1, g2, b2;
+  if (b1 == nbs) { b1 = 0; g1 += gridDim.x; }
+  g2 = g1; b2 = b1 + 1;
+  if (b2 == nbs) { b2 = 0; g2 += gridDim.x; }
+  Slot sa, sb, sc;
+  BatchPos A0 = addr_of(gi, b), A1 = addr_of(g1, b1);
+  if (total > 0) {
+    load_slot<FMT>(geo, A0, W, G, r, j, sa);
+    load_slot<FMT>(geo, A1, W, G, r, j, sb);
+  }
+
+  // ---- prologue part 2: RMSNorm statistics and activation preparation
+  {
+    float inv_rms = 1.f;
+    if (in_regs) {
+      if (p.norm_w != nullptr) {
+        float ss = 0.f;
+#pragma unroll
+        for (int q = 0; q < MAXC; ++q)
+          if (threadIdx.x + q * kBlock < nchunks)
+#pragma unroll
+            for (int e = 0; e < F::kElems; ++e) ss += xr[q][e] * xr[q][e];
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        lds_barrier();
+        ss = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWavesPerBlock; ++w) ss += red[w];
+        inv_rms = 1.f / sqrtf(ss / static_cast<float>(K) + p.eps);
+      }
+#pragma unroll
+      for (int q = 0; q < MAXC; ++q) {
+        const int c = threadIdx.x + q * kBlock;
+        if (c < nchunks) {
+          if (p.norm_w != nullptr) {
+#pragma unroll
+            for (int e2 = 0; e2 < F::kElems / 2; ++e2) {
+              const f16x2 h = as_h2(nr[q][e2]);
+              xr[q][2 * e2] = (inv_rms * xr[q][2 * e2]) * static_cast<float>(h.x);
+              xr[q][2 * e2 + 1] = (inv_rms * xr[q][2 * e2 + 1]) * static_cast<float>(h.y);
+            }
+          }
+          prep_chunk<FMT>(xr[q], lds + c * F::kStride);
+        }
+      }
+    } else {
+      // large K: strided fallback (activations re-read from global)
+      if (p.norm_w != nullptr) {
+        float ss = 0.f;
+        for (int c = threadIdx.x; c < K / 8; c += kBlock) {
+          float v[8];
+          load_x8<XF32>(p.x, c, v);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) red[wave] = ss;
+        lds_barrier();
+        ss = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWavesPerBlock; ++w) ss += red[w];
+        inv_rms = 1.f / sqrtf(ss / static_cast<float>(K) + p.eps);
+      }
+      for (int c = threadIdx.x; c < nchunks; c += kBlock) {
+        float v[F::kElems];
+#pragma unroll
+        for (int e8 = 0; e8 < F::kElems / 8; ++e8) {
+          load_x8<XF32>(p.x, c * (F::kElems / 8) + e8, v + 8 * e8);
+          if (p.norm_w != nullptr) {
+            const u32x4 nw = *reinterpret_cast<const u32x4*>(p.norm_w + (c * (F::kElems / 8) + e8) * 8);
+            const uint32_t nd[4] = {nw.x, nw.y, nw.z, nw.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const f16x2 h = as_h2(nd[q]);
+              v[8 * e8 + 2 * q] = (inv_rms * v[8 * e8 + 2 * q]) * static_cast<float>(h.x);
+              v[8 * e8 + 2 * q + 1] = (inv_rms * v[8 * e8 + 2 * q + 1]) * static_cast<float>(h.y);
+            }
+          }
+        }
+        prep_chunk<FMT>(v, lds + c * F::kStride);
+      }
+    }
+  }
+  lds_barrier();
+
+  const uint32_t* lds_lane = lds + j * F::kStride;
   float acc = 0.f;
-  // One pipeline step: prefetch the successor batch into (WN, GN) while the
-  // current batch in (WC, GC) is consumed.
-#define CPI_GEMV_STEP(WC, GC, WN, GN)                                                          \
+  int done = 0;
+  // One pipeline step: issue position (g2, b2) into SN, consume (gi, b) from SC.
+#define CPI_GEMV_STEP(SC, SN)                                                                  \
   {                                                                                            \
-    int gn = gi, bn = b + 1;                                                                   \
-    if (bn == nbs) { bn = 0; gn += gridDim.x; }                                                \
-    const int tn = gn * tpw + wave / ks;                                                       \
-    const TileCtx tcn = (bn == 0) ? tile_ctx<FMT>(p, tn < tiles ? tn : 0, r, nchunks, row_bytes) \
-                                  : tc;                                                        \
+    const BatchPos A2 = addr_of(g2, b2);                                                       \
+    load_slot<FMT>(geo, A2, W, G, r, j, SN);                                                   \
+    const int t = gi * tpw + wtile;                                                            \
     const bool tile_ok = t < tiles;                                                            \
-    if (gn < groups && tn < tiles) load_batch<FMT>(tcn, b0 + bn, j, nchunks, WN, GN);          \
-    if (tile_ok) acc = compute_batch<FMT>(lds, b0 + b, j, nchunks, WC, GC, acc);               \
+    acc = compute_slot<FMT>(lds_lane, geo, A0, j, SC, acc);                                    \
     if (b == nbs - 1) {                                                                        \
+      TileCtx tc;                                                                              \
+      tc.row = t * kTileRows + r;                                                              \
+      tc.row_ok = tile_ok && tc.row < p.R;                                                     \
       if (ks == 1) {                                                                           \
         if (tile_ok) finish_tile<FMT, EPI>(p, t, r, j, tc, acc);                               \
       } else {                                                                                 \
         const float v = group_sum<kChunkCols>(acc);                                            \
         if (j == 0) part[wave][r] = v;                                                         \
-        __syncthreads();                                                                       \
+        lds_barrier();                                                                         \
         if (seg == 0 && tile_ok) {                                                             \
           float tot = 0.f;                                                                     \
           if (j == 0) {                                                                        \
@@ -447,16 +497,21 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int ks) {
           }                                                                                    \
           finish_tile<FMT, EPI>(p, t, r, j, tc, tot);                                          \
         }                                                                                      \
-        __syncthreads();                                                                       \
+        lds_barrier();                                                                         \
       }                                                                                        \
       acc = 0.f;                                                                               \
     }                                                                                          \
-    gi = gn; b = bn; t = tn; tc = tcn;                                                         \
+    gi = g1; b = b1; g1 = g2; b1 = b2;                                                         \
+    if (++b2 == nbs) { b2 = 0; g2 += gridDim.x; }                                              \
+    A0 = A1; A1 = A2;                                                                          \
+    ++done;                                                                                    \
   }
-  while (gi < groups) {  // uniform across the workgroup
-    CPI_GEMV_STEP(wa, ga, wb, gb)
-    if (gi >= groups) break;
-    CPI_GEMV_STEP(wb, gb, wa, ga)
+  while (done < total) {  // `total` is uniform across the workgroup
+    CPI_GEMV_STEP(sa, sc)
+    if (done >= total) break;
+    CPI_GEMV_STEP(sb, sa)
+    if (done >= total) break;
+    CPI_GEMV_STEP(sc, sb)
   }
 #undef CPI_GEMV_STEP
 }
@@ -475,19 +530,10 @@ size_t lds_bytes(int K) {
 }
 
 template <int FMT, int EPI, bool XF32>
-hipError_t launch(const GemvParams& p, hipStream_t s) {
-  const int tiles = (p.R + kTileRows - 1) / kTileRows;
-  // K-split so that the launch has >= ~2048 waves (8 per CU) when possible.
-  const int steps = (p.K / FmtT<FMT>::kElems + kChunkCols - 1) / kChunkCols;
-  const int nbt = (steps + kUnroll - 1) / kUnroll;
-  int ks = 1;
-  if (g_force_ks > 0) ks = g_force_ks;
-  else if (tiles < 1024 && nbt >= 4) ks = 4;
-  else if (tiles < 2048 && nbt >= 2) ks = 2;
-  if (ks > nbt) ks = nbt >= 4 ? 4 : (nbt >= 2 ? 2 : 1);
-  const int tpw = kWavesPerBlock / ks;
-  int blocks = (tiles + tpw - 1) / tpw;
-  if (blocks > g_max_blocks) blocks = g_max_blocks;
+hipError_t launch(const GemvParams& p_in, hipStream_t s) {
+  const GemvParams& p = p_in;
+  int ks = 1, blocks = 1;
+  plan_launch(p.R, p.K, FmtT<FMT>::kElems, g_max_blocks, g_force_ks, &ks, &blocks);
   const size_t lds = lds_bytes<FMT>(p.K);
   hipLaunchKernelGGL((gemv_kernel<FMT, EPI, XF32>), dim3(blocks), dim3(kBlock), lds, s, p, ks);
   return hipGetLastError();
