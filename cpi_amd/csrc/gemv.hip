@@ -8,19 +8,26 @@
 // (src/engine/llama_engine_graph.cpp:166-480).
 //
 // Design (MI355X):
-//  * Weights stay in the reference's row-major layout; a wave covers 8 rows x
-//    8 sixteen-byte chunks, so each row contributes 128 contiguous bytes per
-//    step and every lane issues one 128-bit load per step.
+//  * Weights stay in the reference's row-major layout.  One wave-wide load is
+//    1 KB of a single row (lane l reads 16-byte chunk pass*64 + l), so every
+//    HBM request is a full, aligned 128-byte line run.
+//  * A wave owns NR rows and a segment of their passes and issues all of its
+//    NR x PP loads (up to 16 x 16 B per lane) before it touches the
+//    activations, so the whole matrix is requested in the first microsecond;
+//    there is no software pipeline for the compiler to serialise.
 //  * The activation vector is converted once per workgroup into a "prepared"
-//    fp16 form in LDS so the inner loop needs no conversion instructions:
-//    a packed weight dword is turned into two fp16 lanes by OR-ing its nibbles
-//    (or bytes) under the exponent of 1024.0 and is consumed by v_dot2_f32_f16
-//    with fp32 accumulation.  The bias that the exponent trick introduces is a
-//    per-chunk constant of x and is pre-subtracted (the dot chain starts at
-//    -C).  High nibbles land at 16x weight, which is compensated by storing
-//    x/16 for those lanes (exact power-of-two scaling).
+//    fp16 form in LDS; a lane reads the prepared chunk of its pass once and
+//    reuses it from registers for all NR rows.  A packed weight dword is turned
+//    into two fp16 lanes by masking its nibbles (or bytes) under the exponent
+//    of 1024.0 and is consumed by v_dot2_f32_f16 with fp32 accumulation.  The
+//    bias that the exponent trick introduces is a per-chunk constant of x and
+//    starts the dot chain.  High nibbles land at 16x weight, which is
+//    compensated by storing x/16 for those lanes (exact power-of-two scaling).
 //  * fp16 weights are dotted against a hi/lo split of the fp32 activation so the
 //    product keeps ~22 bits of the activation.
+//  * Row sums are reduced across the wave with a halving butterfly (NR values
+//    per lane -> one row per lane group) and across the K-segment waves through
+//    LDS in a fixed order, so results are deterministic.
 //  * Optional RMSNorm prologue (statistics in fp32) and fused epilogues
 //    (residual add, SwiGLU, RoPE + KV-cache store) remove the small launches.
 #include <cstdlib>
@@ -32,12 +39,12 @@
 namespace cpi {
 
 constexpr int kBlock = kWave * kWavesPerBlock;
-static_assert(kTileRows * kChunkCols == kWave, "a wave covers 8 rows x 8 chunks");
+static_assert(kPassChunks == kWave, "one chunk per lane per pass");
 
 template <int FMT> struct FmtT;
 template <> struct FmtT<CPI_W_F16> {
   static constexpr int kElems = 8;    // fp16 per 16-byte chunk
-  static constexpr int kStride = 8;   // LDS dwords per chunk: 4 hi + 4 lo
+  static constexpr int kStride = 12;  // LDS dwords per chunk: 4 hi + 4 lo, padded so 8 lanes hit 32 banks
 };
 template <> struct FmtT<CPI_W_I8ROW> {
   static constexpr int kElems = 16;
@@ -137,57 +144,110 @@ __device__ __forceinline__ void prep_chunk(const float* v, uint32_t* dst) {
 }
 
 // ---------------------------------------------------------------------------
-// Dot of one 16-byte weight chunk with its prepared activations.
+// Activation units: 8 consecutive values, raw as loaded.
 // ---------------------------------------------------------------------------
-template <int FMT>
-__device__ __forceinline__ float chunk_dot(const u32x4 w, const uint32_t* p, float acc) {
-  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
-  if constexpr (FMT == CPI_W_F16) {
-    const uint4 ph = *reinterpret_cast<const uint4*>(p);
-    const uint4 pl = *reinterpret_cast<const uint4*>(p + 4);
-    const uint32_t h[4] = {ph.x, ph.y, ph.z, ph.w};
-    const uint32_t l[4] = {pl.x, pl.y, pl.z, pl.w};
-    float t[4];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) t[d] = dot2(wd[d], l[d], dot2(wd[d], h[d], 0.f));
-    return acc + ((t[0] + t[1]) + (t[2] + t[3]));
-  } else if constexpr (FMT == CPI_W_I8ROW) {
-    // (w ^ 0x80808080) & 0x00FF00FF | 0x64006400 == (w & 0x00FF00FF) ^ 0x64806480
-    const uint4 a = *reinterpret_cast<const uint4*>(p);
-    const uint4 b = *reinterpret_cast<const uint4*>(p + 4);
-    const uint32_t pp[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-    float t[4];
-#pragma unroll
-    for (int d = 0; d < 4; ++d)
-      t[d] = dot2(((wd[d] >> 8) & 0x00FF00FFu) ^ 0x64806480u, pp[2 * d + 1],
-                  dot2((wd[d] & 0x00FF00FFu) ^ 0x64806480u, pp[2 * d], 0.f));
-    return acc + (((t[0] + t[1]) + (t[2] + t[3])) + __builtin_bit_cast(float, p[8]));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+template <bool XF32> struct XUnit;
+template <> struct XUnit<true> { f32x4 a, b; };
+template <> struct XUnit<false> { u32x4 a; };
+
+template <bool XF32>
+__device__ __forceinline__ XUnit<XF32> load_unit(const void* x, int u) {
+  XUnit<XF32> r;
+  if constexpr (XF32) {
+    const f32x4* q = reinterpret_cast<const f32x4*>(static_cast<const float*>(x) + 8 * u);
+    r.a = q[0];
+    r.b = q[1];
   } else {
-    // Two's complement nibble n -> offset binary n ^ 8, placed under the
-    // exponent of 1024.0:  (w & M) ^ (0x6400 | 8<<shift) per half.
-    uint32_t pp[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint4 a = reinterpret_cast<const uint4*>(p)[i];
-      pp[4 * i + 0] = a.x;
-      pp[4 * i + 1] = a.y;
-      pp[4 * i + 2] = a.z;
-      pp[4 * i + 3] = a.w;
-    }
-    // four independent dot chains (one per weight dword) keep v_dot2 latency
-    // off the critical path
-    float t[4];
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const uint32_t u = wd[d];
-      const uint32_t u8 = u >> 8;
-      float a = dot2((u & 0x000F000Fu) ^ 0x64086408u, pp[4 * d + 0], 0.f);
-      a = dot2((u & 0x00F000F0u) ^ 0x64806480u, pp[4 * d + 1], a);
-      a = dot2((u8 & 0x000F000Fu) ^ 0x64086408u, pp[4 * d + 2], a);
-      t[d] = dot2((u8 & 0x00F000F0u) ^ 0x64806480u, pp[4 * d + 3], a);
-    }
-    return ((t[0] + t[1]) + (t[2] + t[3])) + __builtin_bit_cast(float, p[16]);  // caller scales
+    r.a = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(x) + 8 * u);
   }
+  return r;
+}
+
+template <bool XF32>
+__device__ __forceinline__ void pin_unit(XUnit<XF32>& r) {
+  if constexpr (XF32) {
+    asm volatile("" : "+v"(r.a), "+v"(r.b));
+  } else {
+    asm volatile("" : "+v"(r.a));
+  }
+}
+
+template <bool XF32>
+__device__ __forceinline__ void unit_floats(const XUnit<XF32>& r, float* v) {
+  if constexpr (XF32) {
+    v[0] = r.a.x; v[1] = r.a.y; v[2] = r.a.z; v[3] = r.a.w;
+    v[4] = r.b.x; v[5] = r.b.y; v[6] = r.b.z; v[7] = r.b.w;
+  } else {
+    const uint32_t d[4] = {r.a.x, r.a.y, r.a.z, r.a.w};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f16x2 h = as_h2(d[q]);
+      v[2 * q] = static_cast<float>(h.x);
+      v[2 * q + 1] = static_cast<float>(h.y);
+    }
+  }
+}
+
+// Prepared form of unit d of a chunk (same values and layout as prep_chunk);
+// returns the unit's share of the chunk's bias sum.
+template <int FMT>
+__device__ __forceinline__ float prep_unit(const float* v, uint32_t* dst, int d) {
+  if constexpr (FMT == CPI_W_F16) {
+    prep_chunk<FMT>(v, dst);
+    return 0.f;
+  } else if constexpr (FMT == CPI_W_I8ROW) {
+    float asum = 0.f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const f16 a0 = static_cast<f16>(v[4 * h + 0]);
+      const f16 a1 = static_cast<f16>(v[4 * h + 1]);
+      const f16 a2 = static_cast<f16>(v[4 * h + 2]);
+      const f16 a3 = static_cast<f16>(v[4 * h + 3]);
+      dst[4 * d + 2 * h + 0] = h2_bits(a0, a2);
+      dst[4 * d + 2 * h + 1] = h2_bits(a1, a3);
+      asum += (static_cast<float>(a0) + static_cast<float>(a1)) +
+              (static_cast<float>(a2) + static_cast<float>(a3));
+    }
+    return asum;
+  } else {
+    const float* e = v;
+    const f16 p0 = static_cast<f16>(e[0]), p4 = static_cast<f16>(e[4]);
+    const f16 p1 = static_cast<f16>(e[1] * 0.0625f), p5 = static_cast<f16>(e[5] * 0.0625f);
+    const f16 p2 = static_cast<f16>(e[2]), p6 = static_cast<f16>(e[6]);
+    const f16 p3 = static_cast<f16>(e[3] * 0.0625f), p7 = static_cast<f16>(e[7] * 0.0625f);
+    dst[4 * d + 0] = h2_bits(p0, p4);
+    dst[4 * d + 1] = h2_bits(p1, p5);
+    dst[4 * d + 2] = h2_bits(p2, p6);
+    dst[4 * d + 3] = h2_bits(p3, p7);
+    const float lo = (static_cast<float>(p0) + static_cast<float>(p4)) +
+                     (static_cast<float>(p2) + static_cast<float>(p6));
+    const float hi = (static_cast<float>(p1) + static_cast<float>(p5)) +
+                     (static_cast<float>(p3) + static_cast<float>(p7));
+    return 1024.f * (lo + hi) + 8.f * (lo + 16.f * hi);
+  }
+}
+
+// Chunk bias from the summed unit shares.
+template <int FMT>
+__device__ __forceinline__ void store_bias(uint32_t* dst, float s) {
+  if constexpr (FMT == CPI_W_I8ROW) dst[8] = __builtin_bit_cast(uint32_t, -1152.f * s);
+  else if constexpr (FMT == CPI_W_I4ROW || FMT == CPI_W_I4G32) dst[16] = __builtin_bit_cast(uint32_t, -s);
+}
+
+// Per-lane select by a constant lane pattern (bit l of `mask` picks `a` in lane l).
+__device__ __forceinline__ float lane_select(uint64_t mask, float a, float b) {
+  float r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(b), "v"(a), "s"(mask));
+  return r;
+}
+
+// Lanes whose index has bit m set.
+constexpr uint64_t lanes_with_bit(int m) {
+  uint64_t r = 0;
+  for (int l = 0; l < 64; ++l)
+    if (l & m) r |= uint64_t{1} << l;
+  return r;
 }
 
 // Eight consecutive activations starting at 8*c (16- or 32-byte aligned).
@@ -217,92 +277,135 @@ __device__ __forceinline__ float load_x(const void* x, int i) {
   else return h2f(static_cast<const uint16_t*>(x)[i]);
 }
 
+
 // ---------------------------------------------------------------------------
-// Kernel pieces.
+// Dot of one 16-byte weight chunk with its prepared activations (registers).
+// A single chain per row: the NR rows of a wave give NR independent chains.
 // ---------------------------------------------------------------------------
-// One pipeline slot: kUnroll weight chunks (and their raw fp16 group scales)
-// of one lane.
-struct Slot {
-  u32x4 w[kUnroll];
-  uint32_t g[kUnroll];
+template <int FMT> struct XPrep {
+  uint32_t v[FmtT<FMT>::kStride];
 };
 
 template <int FMT>
-__device__ __forceinline__ void load_slot(const GemvGeom& g, const BatchPos& bp, const uint8_t* W,
-                                          const uint16_t* G, int r, int j, Slot& s) {
+__device__ __forceinline__ void read_prep(const uint32_t* src, XPrep<FMT>& xp) {
+  constexpr int S = FmtT<FMT>::kStride;
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    s.w[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W + weight_offset(g, bp, r, j, u)));
-    if constexpr (FMT == CPI_W_I4G32) s.g[u] = G[scale_index(g, bp, r, j, u)];
+  for (int i = 0; i < S / 4; ++i) {
+    const uint4 a = reinterpret_cast<const uint4*>(src)[i];
+    xp.v[4 * i + 0] = a.x;
+    xp.v[4 * i + 1] = a.y;
+    xp.v[4 * i + 2] = a.z;
+    xp.v[4 * i + 3] = a.w;
   }
 }
 
+// F16: sum over the chunk, accumulated into `a`.
+// I8ROW / I4: raw dot without the bias constant (the caller adds it).
 template <int FMT>
-__device__ __forceinline__ float compute_slot(const uint32_t* lds_lane, const GemvGeom& g,
-                                              const BatchPos& bp, int j, const Slot& s, float acc) {
-  using F = FmtT<FMT>;
-  const uint32_t* pb = lds_lane + bp.cbase * F::kStride;
+__device__ __forceinline__ float chunk_dot(const u32x4 w, const XPrep<FMT>& xp, float a) {
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+  if constexpr (FMT == CPI_W_F16) {
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    if (!bp.full && bp.cbase + u * kChunkCols + j >= g.nchunks) continue;  // past the row end
-    const uint32_t* pc = pb + u * kChunkCols * F::kStride;
-    if constexpr (FMT == CPI_W_I4G32) acc = fmaf(h2f(static_cast<uint16_t>(s.g[u])), chunk_dot<FMT>(s.w[u], pc, 0.f), acc);
-    else if constexpr (FMT == CPI_W_I4ROW) acc += chunk_dot<FMT>(s.w[u], pc, 0.f);
-    else acc = chunk_dot<FMT>(s.w[u], pc, acc);
+    for (int d = 0; d < 4; ++d) a = dot2(wd[d], xp.v[4 + d], dot2(wd[d], xp.v[d], a));
+    return a;
+  } else if constexpr (FMT == CPI_W_I8ROW) {
+    // (w ^ 0x80808080) & 0x00FF00FF | 0x64006400 == (w & 0x00FF00FF) ^ 0x64806480
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      a = dot2((wd[d] & 0x00FF00FFu) ^ 0x64806480u, xp.v[2 * d], a);
+      a = dot2(((wd[d] >> 8) & 0x00FF00FFu) ^ 0x64806480u, xp.v[2 * d + 1], a);
+    }
+    return a;
+  } else {
+    // Two's complement nibble n -> offset binary n ^ 8 under the exponent of
+    // 1024.0:  (w & M) ^ (0x6400 | 8<<shift) per half.
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t u = wd[d];
+      const uint32_t u8 = u >> 8;
+      a = dot2((u & 0x000F000Fu) ^ 0x64086408u, xp.v[4 * d + 0], a);
+      a = dot2((u & 0x00F000F0u) ^ 0x64806480u, xp.v[4 * d + 1], a);
+      a = dot2((u8 & 0x000F000Fu) ^ 0x64086408u, xp.v[4 * d + 2], a);
+      a = dot2((u8 & 0x00F000F0u) ^ 0x64806480u, xp.v[4 * d + 3], a);
+    }
+    return a;
   }
-  return acc;
 }
 
-struct TileCtx {
-  int row;
-  bool row_ok;
-};
+// Bias constant of a prepared chunk (0 for fp16).
+template <int FMT>
+__device__ __forceinline__ float chunk_bias(const XPrep<FMT>& xp) {
+  if constexpr (FMT == CPI_W_F16) return 0.f;
+  else if constexpr (FMT == CPI_W_I8ROW) return __builtin_bit_cast(float, xp.v[8]);
+  else return __builtin_bit_cast(float, xp.v[16]);
+}
 
-// Reduce the 8 chunk-column partials of each row and run the epilogue.
-template <int FMT, int EPI>
-__device__ __forceinline__ void finish_tile(const GemvParams& p, int t, int r, int j, const TileCtx& tc,
-                                            float acc) {
-  acc = group_sum<kChunkCols>(acc);
-  const int row = tc.row;
-  const bool row_ok = tc.row_ok;
-  if constexpr (FMT == CPI_W_I8ROW || FMT == CPI_W_I4ROW) {
-    const float* sc = static_cast<const float*>(p.scales);
-    acc *= (p.scale_count == 1) ? sc[0] : sc[row_ok ? row : p.R - 1];
+// Sum NR per-lane partials over the wave: returns, in every lane, the total of
+// row (lane >> (6 - log2 NR)) & (NR - 1).  Each halving step trades half of the
+// remaining rows with the partner lane, so NR rows cost NR - 1 + 6 - log2(NR)
+// shuffles instead of 6 NR.
+template <int NR>
+__device__ __forceinline__ float reduce_rows(float (&v)[NR]) {
+  int m = 32;
+#pragma unroll
+  for (int n = NR; n > 1; n >>= 1, m >>= 1) {
+    const uint64_t up = lanes_with_bit(m);
+#pragma unroll
+    for (int i = 0; i < n / 2; ++i) {
+      const float send = lane_select(up, v[i], v[i + n / 2]);
+      const float keep = lane_select(up, v[i + n / 2], v[i]);
+      v[i] = keep + __shfl_xor(send, m, kWave);
+    }
   }
-  if constexpr (EPI == CPI_EPI_STORE_F32) {
-    if (j == 0 && row_ok) static_cast<float*>(p.y)[row] = acc;
-  } else if constexpr (EPI == CPI_EPI_STORE_F16) {
-    if (j == 0 && row_ok) static_cast<uint16_t*>(p.y)[row] = f2h(acc);
-  } else if constexpr (EPI == EPI_DUAL_F16) {
-    if (j == 0 && row_ok) {
+  float s = v[0];
+#pragma unroll
+  for (; m >= 1; m >>= 1) s += __shfl_xor(s, m, kWave);
+  return s;
+}
+
+template <int NR>
+constexpr int log2i() { return NR >= 8 ? 3 : NR >= 4 ? 2 : NR >= 2 ? 1 : 0; }
+
+// ---------------------------------------------------------------------------
+// Per-row epilogue.  Rows of a workgroup are tile-aligned (multiples of 8), so
+// the partner rows of SwiGLU and RoPE pairs are in `fin` of the same block.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void row_epilogue(const GemvParams& p, int epi, int row, int t, const float* fin) {
+  const float acc = fin[t];
+  switch (epi) {
+    case CPI_EPI_STORE_F32: static_cast<float*>(p.y)[row] = acc; break;
+    case CPI_EPI_STORE_F16: static_cast<uint16_t*>(p.y)[row] = f2h(acc); break;
+    case EPI_DUAL_F16:
       if (row < p.rows_a) static_cast<uint16_t*>(p.y)[row] = f2h(acc);
       else static_cast<uint16_t*>(p.y2)[row - p.rows_a] = f2h(acc);
+      break;
+    case CPI_EPI_RESID_ADD: static_cast<float*>(p.y)[row] += acc; break;
+    case CPI_EPI_SWIGLU: {
+      // tile T rows: [w1 4T..4T+3 | w3 4T..4T+3]
+      const int r = row % kTileRows;
+      if (r < 4) {
+        const float u = fin[t + 4];
+        static_cast<float*>(p.y)[(row / kTileRows) * 4 + r] = (acc / (1.f + expf(-acc))) * u;
+      }
+      break;
     }
-  } else if constexpr (EPI == CPI_EPI_RESID_ADD) {
-    if (j == 0 && row_ok) static_cast<float*>(p.y)[row] += acc;
-  } else if constexpr (EPI == CPI_EPI_SWIGLU) {
-    // tile t rows: [w1 4t..4t+3 | w3 4t..4t+3]; partner lane = lane ^ 32.
-    const float other = __shfl_xor(acc, 32, kWave);
-    if (j == 0 && r < 4) {
-      const float g = acc;
-      static_cast<float*>(p.y)[t * 4 + r] = (g / (1.f + expf(-g))) * other;
-    }
-  } else if constexpr (EPI == CPI_EPI_QKV_ROPE) {
-    const float other = __shfl_xor(acc, 32, kWave);
-    const int hd = p.hd;
-    const int half = hd >> 1;
-    const int tiles_per_head = hd / kTileRows;
-    const int q_tiles = p.nh * tiles_per_head;
-    const int k_tiles = p.nkv * tiles_per_head;
-    const int kvdim = p.nkv * hd;
-    const int pos = *p.position;
-    if (j == 0) {
-      if (t < q_tiles + k_tiles) {
-        const bool is_q = t < q_tiles;
-        const int u = is_q ? t : t - q_tiles;
+    case CPI_EPI_QKV_ROPE: {
+      // tile rows: 4 pairs (d, d + hd/2), first members at r < 4.
+      const int T = row / kTileRows;
+      const int r = row % kTileRows;
+      const float other = fin[t ^ 4];
+      const int hd = p.hd;
+      const int half = hd >> 1;
+      const int tiles_per_head = hd / kTileRows;
+      const int q_tiles = p.nh * tiles_per_head;
+      const int k_tiles = p.nkv * tiles_per_head;
+      const int kvdim = p.nkv * hd;
+      const int pos = *p.position;
+      if (T < q_tiles + k_tiles) {
+        const bool is_q = T < q_tiles;
+        const int u = is_q ? T : T - q_tiles;
         const int head = u / tiles_per_head;
-        const int bb = u % tiles_per_head;
-        const int dd = 4 * bb + (r & 3);
+        const int dd = 4 * (u % tiles_per_head) + (r & 3);
         const float c = p.rope_cos[static_cast<size_t>(pos) * half + dd];
         const float s = p.rope_sin[static_cast<size_t>(pos) * half + dd];
         float outv;
@@ -314,206 +417,231 @@ __device__ __forceinline__ void finish_tile(const GemvParams& p, int t, int r, i
           outv = other * s + acc * c;
           d = dd + half;
         }
-        if (is_q) {
-          static_cast<float*>(p.y)[head * hd + d] = outv;
-        } else if (pos < p.max_ctx) {
-          p.k_cache[static_cast<size_t>(pos) * kvdim + head * hd + d] = f2h(outv);
-        }
+        if (is_q) static_cast<float*>(p.y)[head * hd + d] = outv;
+        else if (pos < p.max_ctx) p.k_cache[static_cast<size_t>(pos) * kvdim + head * hd + d] = f2h(outv);
       } else {
-        const int vr = (t - q_tiles - k_tiles) * kTileRows + r;
+        const int vr = (T - q_tiles - k_tiles) * kTileRows + r;
         if (pos < p.max_ctx && vr < kvdim) p.v_cache[static_cast<size_t>(pos) * kvdim + vr] = f2h(acc);
       }
+      break;
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Kernel.  A workgroup's 4 waves cover TPW = 4/KS tiles per iteration, each
-// tile split into KS K-segments (one wave each, equal batch counts, reduced
-// through LDS in a fixed order).  Each wave walks its work as a flat sequence
-// of batches through a ring of three register slots (prefetch distance two);
-// the first two batches are issued before the activation prologue.
+// Kernel.  Workgroup = 4 waves = (4 / KS) row sets of NR rows x KS pass
+// segments.  Per group a wave issues NR x PP 16-byte loads per lane (clamped
+// in-bounds addresses), then consumes them pass by pass.
 // ---------------------------------------------------------------------------
-template <int FMT, int EPI, bool XF32>
-__global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int ks) {
+template <int FMT, bool XF32, int NR, int PP, int MAXU>
+__global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int epi, int ks) {
   using F = FmtT<FMT>;
   extern __shared__ __align__(16) uint32_t lds[];
   __shared__ float red[kWavesPerBlock];
-  __shared__ float part[kWavesPerBlock][kTileRows];
+  __shared__ float part[kWavesPerBlock][kWavesPerBlock * 8];
+  __shared__ float fin[kWavesPerBlock * 8];
 
   const int K = p.K;
-  const GemvGeom geo = make_geom(p.R, K, F::kElems, ks, gridDim.x);
-  const int nchunks = geo.nchunks;
+  const GemvPlan g = make_plan_nrpp(p.R, K, F::kElems, NR, PP, ks);
+  const int nchunks = g.nchunks;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int r = lane / kChunkCols;
-  const int j = lane % kChunkCols;
-  const int tpw = geo.tpw;
-  const int seg = wave % ks;
-  const int tiles = geo.tiles;
-  const int nbs = geo.nbs;
-  const int wtile = wave / ks;
+  const int rs = wave / ks;
+  const int sg = wave % ks;
+  const int block = blockIdx.x;
   const uint8_t* W = static_cast<const uint8_t*>(p.w);
   const uint16_t* G = static_cast<const uint16_t*>(p.scales);
-  const int total = my_groups(geo, blockIdx.x) * nbs;
-  auto addr_of = [&](int g, int bb) { return batch_pos(geo, blockIdx.x, wave, g, bb); };
 
-  // ---- prologue part 1: activations (and norm weights) into registers
-  constexpr int MAXC = 64 / F::kElems;  // chunks per thread held in registers
-  const bool in_regs = nchunks <= MAXC * kBlock;
-  float xr[MAXC][F::kElems];
-  uint32_t nr[MAXC][F::kElems / 2];
+  // ---- activations (and norm weights) in 8-value units: unit u = tid + 256 k
+  const int nunits = K / 8;
+  const bool in_regs = nunits <= MAXU * kBlock;
+  const bool has_norm = p.norm_w != nullptr;
+  XUnit<XF32> xv[MAXU];
+  u32x4 nv[MAXU];
   if (in_regs) {
 #pragma unroll
-    for (int q = 0; q < MAXC; ++q) {
-      const int c = threadIdx.x + q * kBlock;
-      if (c < nchunks) {
+    for (int k = 0; k < MAXU; ++k) {
+      const int u = min(static_cast<int>(threadIdx.x) + k * kBlock, nunits - 1);
+      xv[k] = load_unit<XF32>(p.x, u);
+    }
+    // unconditional, so no branch joins the loaded registers: without a norm
+    // the loads re-read activation bytes that are being fetched anyway
+    const uint16_t* nsrc = has_norm ? p.norm_w : static_cast<const uint16_t*>(p.x);
 #pragma unroll
-        for (int e8 = 0; e8 < F::kElems / 8; ++e8) {
-          load_x8<XF32>(p.x, c * (F::kElems / 8) + e8, &xr[q][8 * e8]);
-          if (p.norm_w != nullptr) {
-            const u32x4 nw = *reinterpret_cast<const u32x4*>(p.norm_w + (c * (F::kElems / 8) + e8) * 8);
-            nr[q][4 * e8 + 0] = nw.x; nr[q][4 * e8 + 1] = nw.y;
-            nr[q][4 * e8 + 2] = nw.z; nr[q][4 * e8 + 3] = nw.w;
-          }
-        }
-      }
+    for (int k = 0; k < MAXU; ++k) {
+      const int u = min(static_cast<int>(threadIdx.x) + k * kBlock, nunits - 1);
+      nv[k] = *reinterpret_cast<const u32x4*>(nsrc + 8 * u);
     }
   }
 
-  // ---- first two batches in flight before the activations are consumed
-  int gi = blockIdx.x, b = 0;
-  int g1 = gi, b1 = 1, g2, b2;
-  if (b1 == nbs) { b1 = 0; g1 += gridDim.x; }
-  g2 = g1; b2 = b1 + 1;
-  if (b2 == nbs) { b2 = 0; g2 += gridDim.x; }
-  Slot sa, sb, sc;
-  BatchPos A0 = addr_of(gi, b), A1 = addr_of(g1, b1);
-  if (total > 0) {
-    load_slot<FMT>(geo, A0, W, G, r, j, sa);
-    load_slot<FMT>(geo, A1, W, G, r, j, sb);
-  }
+  // ---- group-0 weight loads: issued behind the activation loads, so waiting
+  // for the activations (vmcnt = number of weight loads) leaves them in flight
+  u32x4 wv[NR][PP];
+  uint16_t gsc[NR][PP];
+  auto issue = [&](int grp) {
+#pragma unroll
+    for (int q = 0; q < PP; ++q) {
+      const int pass = clamp_pass(g, sg, plan_pass(g, sg, grp, q));
+      const int c = clamp_chunk(g, pass, lane);
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        const int row = clamp_row(g, plan_row(g, block, rs, i));
+        if constexpr (FMT == CPI_W_I4G32) gsc[i][q] = G[scale_index(g, row, c)];
+        wv[i][q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W + weight_offset(g, row, c)));
+      }
+    }
+  };
+  issue(0);
 
-  // ---- prologue part 2: RMSNorm statistics and activation preparation
-  {
+  // ---- RMSNorm statistics and activation preparation into LDS
+  if (in_regs) {
+    // The empty asm makes every use of the activations follow the weight
+    // loads in program order (the compiler would otherwise convert them, and
+    // wait for them, before issuing the weights).
+#pragma unroll
+    for (int k = 0; k < MAXU; ++k) {
+      pin_unit<XF32>(xv[k]);
+      asm volatile("" : "+v"(nv[k]));
+    }
     float inv_rms = 1.f;
-    if (in_regs) {
-      if (p.norm_w != nullptr) {
-        float ss = 0.f;
+    if (has_norm) {
+      float ss = 0.f;
 #pragma unroll
-        for (int q = 0; q < MAXC; ++q)
-          if (threadIdx.x + q * kBlock < nchunks)
-#pragma unroll
-            for (int e = 0; e < F::kElems; ++e) ss += xr[q][e] * xr[q][e];
-        ss = wave_sum(ss);
-        if (lane == 0) red[wave] = ss;
-        lds_barrier();
-        ss = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWavesPerBlock; ++w) ss += red[w];
-        inv_rms = 1.f / sqrtf(ss / static_cast<float>(K) + p.eps);
-      }
-#pragma unroll
-      for (int q = 0; q < MAXC; ++q) {
-        const int c = threadIdx.x + q * kBlock;
-        if (c < nchunks) {
-          if (p.norm_w != nullptr) {
-#pragma unroll
-            for (int e2 = 0; e2 < F::kElems / 2; ++e2) {
-              const f16x2 h = as_h2(nr[q][e2]);
-              xr[q][2 * e2] = (inv_rms * xr[q][2 * e2]) * static_cast<float>(h.x);
-              xr[q][2 * e2 + 1] = (inv_rms * xr[q][2 * e2 + 1]) * static_cast<float>(h.y);
-            }
-          }
-          prep_chunk<FMT>(xr[q], lds + c * F::kStride);
-        }
-      }
-    } else {
-      // large K: strided fallback (activations re-read from global)
-      if (p.norm_w != nullptr) {
-        float ss = 0.f;
-        for (int c = threadIdx.x; c < K / 8; c += kBlock) {
+      for (int k = 0; k < MAXU; ++k) {
+        if (static_cast<int>(threadIdx.x) + k * kBlock < nunits) {
           float v[8];
-          load_x8<XF32>(p.x, c, v);
+          unit_floats<XF32>(xv[k], v);
 #pragma unroll
           for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
         }
-        ss = wave_sum(ss);
-        if (lane == 0) red[wave] = ss;
-        lds_barrier();
-        ss = 0.f;
-#pragma unroll
-        for (int w = 0; w < kWavesPerBlock; ++w) ss += red[w];
-        inv_rms = 1.f / sqrtf(ss / static_cast<float>(K) + p.eps);
       }
-      for (int c = threadIdx.x; c < nchunks; c += kBlock) {
-        float v[F::kElems];
+      ss = wave_sum(ss);
+      if (lane == 0) red[wave] = ss;
+      lds_barrier();
+      ss = 0.f;
 #pragma unroll
-        for (int e8 = 0; e8 < F::kElems / 8; ++e8) {
-          load_x8<XF32>(p.x, c * (F::kElems / 8) + e8, v + 8 * e8);
-          if (p.norm_w != nullptr) {
-            const u32x4 nw = *reinterpret_cast<const u32x4*>(p.norm_w + (c * (F::kElems / 8) + e8) * 8);
-            const uint32_t nd[4] = {nw.x, nw.y, nw.z, nw.w};
+      for (int w = 0; w < kWavesPerBlock; ++w) ss += red[w];
+      inv_rms = 1.f / sqrtf(ss / static_cast<float>(K) + p.eps);
+    }
+    constexpr int UPC = F::kElems / 8;  // units per chunk: adjacent lanes
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const f16x2 h = as_h2(nd[q]);
-              v[8 * e8 + 2 * q] = (inv_rms * v[8 * e8 + 2 * q]) * static_cast<float>(h.x);
-              v[8 * e8 + 2 * q + 1] = (inv_rms * v[8 * e8 + 2 * q + 1]) * static_cast<float>(h.y);
-            }
+    for (int k = 0; k < MAXU; ++k) {
+      const int u = static_cast<int>(threadIdx.x) + k * kBlock;
+      const bool ok = u < nunits;
+      float v[8];
+      unit_floats<XF32>(xv[k], v);
+      if (has_norm) {
+        const uint32_t nd[4] = {nv[k].x, nv[k].y, nv[k].z, nv[k].w};
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+          const f16x2 h = as_h2(nd[e2]);
+          v[2 * e2] = (inv_rms * v[2 * e2]) * static_cast<float>(h.x);
+          v[2 * e2 + 1] = (inv_rms * v[2 * e2 + 1]) * static_cast<float>(h.y);
+        }
+      }
+      uint32_t* dst = lds + (u / UPC) * F::kStride;
+      float cpart = 0.f;
+      if (ok) cpart = prep_unit<FMT>(v, dst, u % UPC);
+      if constexpr (UPC > 1) {
+        // chunk bias: sum over the chunk's units (lanes u..u+UPC-1, all valid or all not)
+        cpart = group_sum<UPC>(cpart);
+        if (ok && u % UPC == 0) store_bias<FMT>(dst, cpart);
+      }
+    }
+  } else {
+    // large K: strided loop (activations re-read from global after the weights)
+    float inv_rms = 1.f;
+    if (has_norm) {
+      float ss = 0.f;
+      for (int c = threadIdx.x; c < nunits; c += kBlock) {
+        float v[8];
+        load_x8<XF32>(p.x, c, v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) red[wave] = ss;
+      lds_barrier();
+      ss = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWavesPerBlock; ++w) ss += red[w];
+      inv_rms = 1.f / sqrtf(ss / static_cast<float>(K) + p.eps);
+    }
+    for (int c = threadIdx.x; c < nchunks; c += kBlock) {
+      float v[F::kElems];
+#pragma unroll
+      for (int e8 = 0; e8 < F::kElems / 8; ++e8) {
+        load_x8<XF32>(p.x, c * (F::kElems / 8) + e8, v + 8 * e8);
+        if (has_norm) {
+          const u32x4 nw = *reinterpret_cast<const u32x4*>(p.norm_w + (c * (F::kElems / 8) + e8) * 8);
+          const uint32_t nd[4] = {nw.x, nw.y, nw.z, nw.w};
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f16x2 h = as_h2(nd[q]);
+            v[8 * e8 + 2 * q] = (inv_rms * v[8 * e8 + 2 * q]) * static_cast<float>(h.x);
+            v[8 * e8 + 2 * q + 1] = (inv_rms * v[8 * e8 + 2 * q + 1]) * static_cast<float>(h.y);
           }
         }
-        prep_chunk<FMT>(v, lds + c * F::kStride);
       }
+      prep_chunk<FMT>(v, lds + c * F::kStride);
     }
   }
   lds_barrier();
 
-  const uint32_t* lds_lane = lds + j * F::kStride;
-  float acc = 0.f;
-  int done = 0;
-  // One pipeline step: issue position (g2, b2) into SN, consume (gi, b) from SC.
-#define CPI_GEMV_STEP(SC, SN)                                                                  \
-  {                                                                                            \
-    const BatchPos A2 = addr_of(g2, b2);                                                       \
-    load_slot<FMT>(geo, A2, W, G, r, j, SN);                                                   \
-    const int t = gi * tpw + wtile;                                                            \
-    const bool tile_ok = t < tiles;                                                            \
-    acc = compute_slot<FMT>(lds_lane, geo, A0, j, SC, acc);                                    \
-    if (b == nbs - 1) {                                                                        \
-      TileCtx tc;                                                                              \
-      tc.row = t * kTileRows + r;                                                              \
-      tc.row_ok = tile_ok && tc.row < p.R;                                                     \
-      if (ks == 1) {                                                                           \
-        if (tile_ok) finish_tile<FMT, EPI>(p, t, r, j, tc, acc);                               \
-      } else {                                                                                 \
-        const float v = group_sum<kChunkCols>(acc);                                            \
-        if (j == 0) part[wave][r] = v;                                                         \
-        lds_barrier();                                                                         \
-        if (seg == 0 && tile_ok) {                                                             \
-          float tot = 0.f;                                                                     \
-          if (j == 0) {                                                                        \
-            tot = part[wave][r];                                                               \
-            for (int s2 = 1; s2 < ks; ++s2) tot += part[wave + s2][r];                         \
-          }                                                                                    \
-          finish_tile<FMT, EPI>(p, t, r, j, tc, tot);                                          \
-        }                                                                                      \
-        lds_barrier();                                                                         \
-      }                                                                                        \
-      acc = 0.f;                                                                               \
-    }                                                                                          \
-    gi = g1; b = b1; g1 = g2; b1 = b2;                                                         \
-    if (++b2 == nbs) { b2 = 0; g2 += gridDim.x; }                                              \
-    A0 = A1; A1 = A2;                                                                          \
-    ++done;                                                                                    \
+  // ---- main loop
+  float acc[NR];
+#pragma unroll
+  for (int i = 0; i < NR; ++i) acc[i] = 0.f;
+  float bias_sum = 0.f;  // per-row-scale formats: bias constants, shared by all rows
+  auto compute = [&](int grp) {
+#pragma unroll
+    for (int q = 0; q < PP; ++q) {
+      const int pass = plan_pass(g, sg, grp, q);
+      if (!pass_valid(g, sg, pass)) continue;  // wave-uniform
+      const int c = pass * kPassChunks + lane;
+      if (c < nchunks) {
+        XPrep<FMT> xp;
+        read_prep<FMT>(lds + c * F::kStride, xp);
+        if constexpr (FMT == CPI_W_I4G32) {
+          const float b = chunk_bias<FMT>(xp);
+#pragma unroll
+          for (int i = 0; i < NR; ++i) acc[i] = fmaf(h2f(gsc[i][q]), chunk_dot<FMT>(wv[i][q], xp, b), acc[i]);
+        } else {
+          if constexpr (FMT != CPI_W_F16) bias_sum += chunk_bias<FMT>(xp);
+#pragma unroll
+          for (int i = 0; i < NR; ++i) acc[i] = chunk_dot<FMT>(wv[i][q], xp, acc[i]);
+        }
+      }
+    }
+  };
+  compute(0);
+  for (int grp = 1; grp < g.ng; ++grp) {
+    issue(grp);
+    compute(grp);
   }
-  while (done < total) {  // `total` is uniform across the workgroup
-    CPI_GEMV_STEP(sa, sc)
-    if (done >= total) break;
-    CPI_GEMV_STEP(sb, sa)
-    if (done >= total) break;
-    CPI_GEMV_STEP(sc, sb)
+  if constexpr (FMT == CPI_W_I8ROW || FMT == CPI_W_I4ROW) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) acc[i] += bias_sum;
   }
-#undef CPI_GEMV_STEP
+
+  // ---- reductions: wave butterfly, then K segments in a fixed order
+  constexpr int L2 = log2i<NR>();
+  const float s = reduce_rows<NR>(acc);
+  if ((lane & ((kWave >> L2) - 1)) == 0) part[sg][rs * NR + (lane >> (6 - L2))] = s;
+  lds_barrier();
+  const int t = threadIdx.x;
+  const int row = block * g.rb + t;
+  if (t < g.rb) {
+    float v = part[0][t];
+    for (int s2 = 1; s2 < ks; ++s2) v += part[s2][t];
+    if constexpr (FMT == CPI_W_I8ROW || FMT == CPI_W_I4ROW) {
+      const float* sc = static_cast<const float*>(p.scales);
+      v *= (p.scale_count == 1) ? sc[0] : sc[row < p.R ? row : p.R - 1];
+    }
+    fin[t] = v;
+  }
+  lds_barrier();
+  if (t < g.rb && row < p.R) row_epilogue(p, epi, row, t, fin);
 }
 
 // ---------------------------------------------------------------------------
@@ -521,7 +649,7 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int ks) {
 // ---------------------------------------------------------------------------
 namespace {
 
-int g_max_blocks = 4096;
+int g_force_shape = -1;
 int g_force_ks = 0;
 
 template <int FMT>
@@ -529,43 +657,64 @@ size_t lds_bytes(int K) {
   return static_cast<size_t>(K / FmtT<FMT>::kElems) * FmtT<FMT>::kStride * sizeof(uint32_t);
 }
 
-template <int FMT, int EPI, bool XF32>
-hipError_t launch(const GemvParams& p_in, hipStream_t s) {
-  const GemvParams& p = p_in;
-  int ks = 1, blocks = 1;
-  plan_launch(p.R, p.K, FmtT<FMT>::kElems, g_max_blocks, g_force_ks, &ks, &blocks);
-  const size_t lds = lds_bytes<FMT>(p.K);
-  hipLaunchKernelGGL((gemv_kernel<FMT, EPI, XF32>), dim3(blocks), dim3(kBlock), lds, s, p, ks);
+template <int FMT, bool XF32, int NR, int PP, int MAXU>
+hipError_t launch_kernel(const GemvParams& p, int epi, const GemvPlan& g, size_t lds, hipStream_t s) {
+  static size_t lds_set = 0;  // per instantiation: raise the dynamic-LDS limit once
+  if (lds > 64 * 1024 && lds > lds_set) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<FMT, XF32, NR, PP, MAXU>),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (e != hipSuccess) return e;
+    lds_set = lds;
+  }
+  hipLaunchKernelGGL((gemv_kernel<FMT, XF32, NR, PP, MAXU>), dim3(g.grid), dim3(kBlock), lds, s, p, epi, g.ks);
   return hipGetLastError();
 }
 
+// Activation units held in registers per thread: 2 covers K <= 4096, 8 covers
+// K <= 16384; larger K takes the strided path.
+template <int FMT, bool XF32, int NR, int PP>
+hipError_t launch_shape(const GemvParams& p, int epi, const GemvPlan& g, size_t lds, hipStream_t s) {
+  if (p.K <= 2 * 8 * kBlock) return launch_kernel<FMT, XF32, NR, PP, 2>(p, epi, g, lds, s);
+  return launch_kernel<FMT, XF32, NR, PP, 8>(p, epi, g, lds, s);
+}
+
 template <int FMT, bool XF32>
-hipError_t dispatch_epi(int epi, const GemvParams& p, hipStream_t s) {
-  switch (epi) {
-    case CPI_EPI_STORE_F32: return launch<FMT, CPI_EPI_STORE_F32, XF32>(p, s);
-    case CPI_EPI_STORE_F16: return launch<FMT, CPI_EPI_STORE_F16, XF32>(p, s);
-    case CPI_EPI_RESID_ADD: return launch<FMT, CPI_EPI_RESID_ADD, XF32>(p, s);
-    case CPI_EPI_SWIGLU: return launch<FMT, CPI_EPI_SWIGLU, XF32>(p, s);
-    case CPI_EPI_QKV_ROPE: return launch<FMT, CPI_EPI_QKV_ROPE, XF32>(p, s);
-    case EPI_DUAL_F16: return launch<FMT, EPI_DUAL_F16, XF32>(p, s);
+hipError_t launch(const GemvParams& p, int epi, hipStream_t s) {
+  const GemvPlan g = plan_launch(p.R, p.K, FmtT<FMT>::kElems, g_force_shape, g_force_ks);
+  const size_t lds = lds_bytes<FMT>(p.K);
+  if (lds > 160 * 1024) return hipErrorInvalidValue;  // K too large for the LDS plan
+  static_assert(kNumShapes == 6, "shape table and dispatch must agree");
+  switch (g.shape) {
+    case 0: return launch_shape<FMT, XF32, kShapes[0].nr, kShapes[0].pp>(p, epi, g, lds, s);
+    case 1: return launch_shape<FMT, XF32, kShapes[1].nr, kShapes[1].pp>(p, epi, g, lds, s);
+    case 2: return launch_shape<FMT, XF32, kShapes[2].nr, kShapes[2].pp>(p, epi, g, lds, s);
+    case 3: return launch_shape<FMT, XF32, kShapes[3].nr, kShapes[3].pp>(p, epi, g, lds, s);
+    case 4: return launch_shape<FMT, XF32, kShapes[4].nr, kShapes[4].pp>(p, epi, g, lds, s);
+    case 5: return launch_shape<FMT, XF32, kShapes[5].nr, kShapes[5].pp>(p, epi, g, lds, s);
   }
   return hipErrorInvalidValue;
 }
 
 template <int FMT>
 hipError_t dispatch_x(int epi, bool xf32, const GemvParams& p, hipStream_t s) {
-  return xf32 ? dispatch_epi<FMT, true>(epi, p, s) : dispatch_epi<FMT, false>(epi, p, s);
+  switch (epi) {
+    case CPI_EPI_STORE_F32: case CPI_EPI_STORE_F16: case CPI_EPI_RESID_ADD:
+    case CPI_EPI_SWIGLU: case CPI_EPI_QKV_ROPE: case EPI_DUAL_F16: break;
+    default: return hipErrorInvalidValue;
+  }
+  return xf32 ? launch<FMT, true>(p, epi, s) : launch<FMT, false>(p, epi, s);
 }
 
 }  // namespace
 
-void gemv_set_max_blocks(int n) { g_max_blocks = n > 0 ? n : 4096; }
+// Tuning overrides: shape index into kShapes (-1 = automatic), K-split (0 = automatic).
+void gemv_set_shape(int n) { g_force_shape = (n >= 0 && n < kNumShapes) ? n : -1; }
 void gemv_set_ksplit(int n) { g_force_ks = (n == 1 || n == 2 || n == 4) ? n : 0; }
 
 hipError_t gemv_launch(int wfmt, int epi, bool xf32, const GemvParams& p, hipStream_t s) {
   static const bool env_once = [] {
     if (const char* v = getenv("CPI_GEMV_KSPLIT")) gemv_set_ksplit(atoi(v));
-    if (const char* v = getenv("CPI_GEMV_MAX_BLOCKS")) gemv_set_max_blocks(atoi(v));
+    if (const char* v = getenv("CPI_GEMV_SHAPE")) gemv_set_shape(atoi(v));
     return true;
   }();
   (void)env_once;
@@ -587,6 +736,5 @@ int gemv_elems_per_chunk(int wfmt) {
   }
   return 0;
 }
-
 
 }  // namespace cpi

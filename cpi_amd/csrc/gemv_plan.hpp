@@ -1,12 +1,17 @@
-// Launch geometry and address arithmetic of the GEMV kernel, shared by the
-// device code and by a host-side bounds checker (tests/test_gemv_addressing.py
+// Launch plan and address arithmetic of the GEMV kernel, shared by the device
+// code and by a host-side bounds checker (tests/test_gemv_addressing.py
 // compiles this header with g++ and enumerates every load the kernel issues).
 //
-// Layout: W is row-major [R, K] in 16-byte chunks (kElems values per chunk,
-// nchunks = K / kElems per row).  A wave owns 8-row tiles; lane (r = lane/8,
-// j = lane%8) reads chunk (batch*kUnroll + u)*8 + j of row tile*8 + r.
+// Layout: W is row-major [R, K] in 16-byte chunks (`elems` values per chunk,
+// nchunks = K / elems per row).  A "pass" is 64 consecutive chunks of one row:
+// lane l of a wave reads chunk pass*64 + l, so one wave-wide load is 1 KB of a
+// single row.  A wave owns NR rows and a segment of the passes of those rows;
+// the KS waves that share rows split the passes and are reduced through LDS.
+// Each wave issues NR x PP loads per group and runs NG groups.
+//
 // Every offset below is non-negative and in bounds: rows past R re-read row
-// R-1 and chunks past the row end re-read the row's last chunk.
+// R-1, chunks past the row end re-read the row's last chunk, passes past the
+// wave's segment re-read its last pass.  Such loads are never accumulated.
 #pragma once
 
 #include <cstddef>
@@ -20,108 +25,120 @@
 
 namespace cpi {
 
-constexpr int kChunkCols = 8;                 // 16-byte chunks per row per step
-constexpr int kTileRows = 8;                  // rows per wave tile (64 lanes / 8)
+constexpr int kPassChunks = 64;   // chunks per pass (one per lane)
 constexpr int kWavesPerBlock = 4;
-constexpr int kUnroll = 4;                    // steps per batch
+constexpr int kTileRows = 8;      // row granularity of the fused epilogues
+constexpr int kMaxLoads = 16;     // NR * PP: 16-byte loads a lane keeps in flight
 
-struct GemvGeom {
-  int R, K, elems;        // rows, columns, values per 16-byte chunk
-  int ks;                 // K-segments per tile (waves cooperating on a tile)
-  int grid;               // workgroups
-  int tpw;                // tiles per workgroup iteration = 4 / ks
-  int tiles, nchunks, steps, nbt, nbs, groups;
+// (NR, PP) shapes the kernel is instantiated for.
+struct WaveShape {
+  int nr, pp;
+};
+constexpr WaveShape kShapes[] = {{8, 2}, {8, 1}, {4, 4}, {4, 3}, {4, 1}, {2, 8}};
+constexpr int kNumShapes = sizeof(kShapes) / sizeof(kShapes[0]);
+
+struct GemvPlan {
+  int R, K, elems;
+  int shape;      // index into kShapes
+  int nr, pp;     // rows per wave, passes per group
+  int ks;         // waves sharing a row set (pass segments)
+  int ng;         // groups per wave
+  int rb;         // rows per workgroup = nr * 4 / ks
+  int grid;       // workgroups
+  int nchunks, np, pps;  // chunks per row, passes per row, passes per segment
   uint32_t row_bytes;
 };
 
-CPI_HD inline GemvGeom make_geom(int R, int K, int elems, int ks, int grid) {
-  GemvGeom g;
+CPI_HD inline GemvPlan make_plan_nrpp(int R, int K, int elems, int nr, int pp, int ks) {
+  GemvPlan g;
   g.R = R;
   g.K = K;
   g.elems = elems;
+  g.shape = -1;
+  g.nr = nr;
+  g.pp = pp;
   g.ks = ks;
-  g.grid = grid;
-  g.tpw = kWavesPerBlock / ks;
-  g.tiles = (R + kTileRows - 1) / kTileRows;
   g.nchunks = K / elems;
-  g.steps = (g.nchunks + kChunkCols - 1) / kChunkCols;
-  g.nbt = (g.steps + kUnroll - 1) / kUnroll;
-  g.nbs = (g.nbt + ks - 1) / ks;
-  g.groups = (g.tiles + g.tpw - 1) / g.tpw;
+  g.np = (g.nchunks + kPassChunks - 1) / kPassChunks;
+  g.pps = (g.np + ks - 1) / ks;
+  g.ng = (g.pps + g.pp - 1) / g.pp;
+  g.rb = g.nr * kWavesPerBlock / ks;
+  g.grid = (R + g.rb - 1) / g.rb;
   g.row_bytes = static_cast<uint32_t>(K) * 16u / static_cast<uint32_t>(elems);
   return g;
 }
 
-// Host launch plan: K-split so the launch has >= ~2048 waves when possible.
-inline void plan_launch(int R, int K, int elems, int max_blocks, int force_ks, int* ks_out,
-                        int* grid_out) {
-  const int tiles = (R + kTileRows - 1) / kTileRows;
-  const int steps = (K / elems + kChunkCols - 1) / kChunkCols;
-  const int nbt = (steps + kUnroll - 1) / kUnroll;
-  int ks = 1;
-  if (force_ks > 0) ks = force_ks;
-  else if (tiles < 1024 && nbt >= 4) ks = 4;
-  else if (tiles < 1536 && nbt >= 2) ks = 2;
-  if (ks > nbt) ks = nbt >= 4 ? 4 : (nbt >= 2 ? 2 : 1);
-  const int tpw = kWavesPerBlock / ks;
-  int grid = (tiles + tpw - 1) / tpw;
-  if (grid > max_blocks) grid = max_blocks;
-  if (grid < 1) grid = 1;
-  *ks_out = ks;
-  *grid_out = grid;
+CPI_HD inline GemvPlan make_plan(int R, int K, int elems, int shape, int ks) {
+  GemvPlan g = make_plan_nrpp(R, K, elems, kShapes[shape].nr, kShapes[shape].pp, ks);
+  g.shape = shape;
+  return g;
 }
 
-// Number of tile groups workgroup `block` processes, and the last one.
-CPI_HD inline int my_groups(const GemvGeom& g, int block) {
-  return g.groups > block ? (g.groups - block + g.grid - 1) / g.grid : 0;
+CPI_HD inline bool plan_valid(int shape, int ks) {
+  const int nr = kShapes[shape].nr;
+  const int rb = nr * kWavesPerBlock / ks;
+  return nr * kWavesPerBlock % ks == 0 && rb >= kTileRows && rb % kTileRows == 0;
 }
 
-// Wave-uniform description of one batch position.
-struct BatchPos {
-  int tile;    // tile index actually read (clamped into range)
-  int row0;    // first row of the tile
-  int rmax;    // last valid row offset inside the tile (< 8 only for the last tile)
-  int cbase;   // first chunk of the batch (may be >= nchunks for an empty batch)
-  bool full;   // all chunks of the batch are < nchunks
-};
-
-// Batch (group gpos, batch bb of the wave's segment); positions past the
-// workgroup's work are clamped to its last batch (their loads are discarded).
-CPI_HD inline BatchPos batch_pos(const GemvGeom& g, int block, int wave, int gpos, int bb) {
-  const int mg = my_groups(g, block);
-  const int last_g = block + (mg > 0 ? mg - 1 : 0) * g.grid;
-  if (gpos > last_g) {
-    gpos = last_g;
-    bb = g.nbs - 1;
+// Host plan: all loads of a wave in flight at once where the shape allows,
+// full pass utilisation, and enough waves (>= 2 per SIMD of 256 CUs) to fill
+// the chip.  force_shape / force_ks (>= 0 / > 0) override the choice.
+inline GemvPlan plan_launch(int R, int K, int elems, int force_shape, int force_ks) {
+  double best = -1.0;
+  GemvPlan bp = make_plan(R, K, elems, 0, 1);
+  for (int s = 0; s < kNumShapes; ++s) {
+    if (force_shape >= 0 && s != force_shape) continue;
+    for (int ks = 1; ks <= 4; ks *= 2) {
+      if (force_ks > 0 && ks != force_ks) continue;
+      if (!plan_valid(s, ks)) continue;
+      const GemvPlan g = make_plan(R, K, elems, s, ks);
+      const double util = static_cast<double>(g.np) / (static_cast<double>(g.ks) * g.ng * g.pp);
+      const double waves = static_cast<double>(g.grid) * kWavesPerBlock;
+      double score = util * (waves >= 2048.0 ? 1.0 : waves / 2048.0);
+      if (g.ng > 1) score *= 0.9;
+      if (g.nr * g.pp < 8) score *= 0.9;
+      // ties: more bytes per wave in flight, then more rows per wave
+      score += 1e-3 * g.nr * g.pp + 1e-4 * g.nr;
+      if (score > best) {
+        best = score;
+        bp = g;
+      }
+    }
   }
-  int t = gpos * g.tpw + wave / g.ks;
-  if (t >= g.tiles) t = g.tiles - 1;
-  BatchPos b;
-  b.tile = t;
-  b.row0 = t * kTileRows;
-  const int last = g.R - 1 - b.row0;
-  b.rmax = last < kTileRows - 1 ? last : kTileRows - 1;
-  b.cbase = ((wave % g.ks) * g.nbs + bb) * kUnroll * kChunkCols;
-  b.full = b.cbase + kUnroll * kChunkCols <= g.nchunks;
-  return b;
+  return bp;
 }
 
-// Chunk index (within its row) that lane (r, j) reads for step u of batch b.
-CPI_HD inline int lane_chunk(const GemvGeom& g, const BatchPos& b, int j, int u) {
-  const int c = b.cbase + u * kChunkCols + j;
+// Row that wave-row slot i of row set `rs` in `block` reads (clamped to R-1),
+// and the unclamped row it stands for.
+CPI_HD inline int plan_row(const GemvPlan& g, int block, int rs, int i) {
+  return block * g.rb + rs * g.nr + i;
+}
+CPI_HD inline int clamp_row(const GemvPlan& g, int row) { return row < g.R ? row : g.R - 1; }
+
+// Pass q of group grp of segment sg: its index, clamped into the segment, and
+// whether it is a real pass of the segment.
+CPI_HD inline int plan_pass(const GemvPlan& g, int sg, int grp, int q) {
+  return sg * g.pps + grp * g.pp + q;
+}
+CPI_HD inline bool pass_valid(const GemvPlan& g, int sg, int pass) {
+  const int end = (sg + 1) * g.pps < g.np ? (sg + 1) * g.pps : g.np;
+  return pass < end;
+}
+CPI_HD inline int clamp_pass(const GemvPlan& g, int sg, int pass) {
+  int end = (sg + 1) * g.pps < g.np ? (sg + 1) * g.pps : g.np;
+  if (end <= sg * g.pps) end = g.np;  // empty segment: re-read the row's last pass
+  return pass < end ? pass : end - 1;
+}
+CPI_HD inline int clamp_chunk(const GemvPlan& g, int pass, int lane) {
+  const int c = pass * kPassChunks + lane;
   return c < g.nchunks ? c : g.nchunks - 1;
 }
 
-CPI_HD inline int lane_row(const BatchPos& b, int r) { return b.row0 + (r < b.rmax ? r : b.rmax); }
-
-// Byte offset of the 16-byte weight chunk, and element index of its fp16
-// group scale (I4G32: one scale per chunk).
-CPI_HD inline size_t weight_offset(const GemvGeom& g, const BatchPos& b, int r, int j, int u) {
-  return static_cast<size_t>(lane_row(b, r)) * g.row_bytes + static_cast<size_t>(lane_chunk(g, b, j, u)) * 16u;
+CPI_HD inline size_t weight_offset(const GemvPlan& g, int row_c, int chunk_c) {
+  return static_cast<size_t>(row_c) * g.row_bytes + static_cast<size_t>(chunk_c) * 16u;
 }
-CPI_HD inline size_t scale_index(const GemvGeom& g, const BatchPos& b, int r, int j, int u) {
-  return static_cast<size_t>(lane_row(b, r)) * static_cast<size_t>(g.nchunks) +
-         static_cast<size_t>(lane_chunk(g, b, j, u));
+CPI_HD inline size_t scale_index(const GemvPlan& g, int row_c, int chunk_c) {
+  return static_cast<size_t>(row_c) * static_cast<size_t>(g.nchunks) + static_cast<size_t>(chunk_c);
 }
 
 }  // namespace cpi

@@ -1,7 +1,7 @@
 """CPU replay of the GEMV kernel's addressing (cpi_amd/csrc/gemv_plan.hpp,
 the same header the kernel includes): no load leaves the weight / scale
 buffers and every (row, chunk) is accumulated exactly once, for the shapes
-the engine and tests use and for odd shapes, launch caps and K-splits."""
+the engine and tests use and for odd shapes, wave shapes and K-splits."""
 import os
 import subprocess
 
@@ -28,15 +28,19 @@ SHAPES = [(12288, 4096), (22016, 4096), (4096, 11008), (4096, 4096), (32000, 409
 def test_addressing_default_plan(checker, R, K, elems):
     if K % elems:
         pytest.skip("K not a multiple of the chunk width")
-    out = subprocess.run([checker, str(R), str(K), str(elems), "4096", "0"], capture_output=True, text=True)
+    out = subprocess.run([checker, str(R), str(K), str(elems), "-1", "0"], capture_output=True, text=True)
     assert out.returncode == 0, out.stdout
 
 
 @pytest.mark.parametrize("ks", [1, 2, 4])
-@pytest.mark.parametrize("max_blocks", [1, 3, 64, 4096])
-@pytest.mark.parametrize("R,K", [(300, 544), (4096, 11008), (37, 96), (1000, 4096)])
-def test_addressing_forced(checker, R, K, ks, max_blocks):
-    for elems in (8, 32):
-        out = subprocess.run([checker, str(R), str(K), str(elems), str(max_blocks), str(ks)], capture_output=True,
+@pytest.mark.parametrize("shape", range(6))
+@pytest.mark.parametrize("R,K", [(300, 544), (4096, 11008), (40, 96), (1000, 4096), (24, 8192)])
+def test_addressing_forced(checker, R, K, ks, shape):
+    """Every (wave shape, K-split) the kernel can be forced into; invalid
+    combinations fall back to a valid plan, which must also be correct."""
+    for elems in (8, 16, 32):
+        if K % elems:
+            continue
+        out = subprocess.run([checker, str(R), str(K), str(elems), str(shape), str(ks)], capture_output=True,
                              text=True)
         assert out.returncode == 0, out.stdout
