@@ -1,6 +1,7 @@
 // Decode attention for gfx950: exact online softmax, split-K over context,
 // one workgroup per (KV head, context split) serving all query heads of the
-// GQA group, followed by a log-sum-exp merge.
+// GQA group; the last workgroup of a KV head to finish merges the splits
+// (log-sum-exp) in the same launch.
 //
 // Replaces src/kernels/kernels_attention_decode.cu:194-446 (tiled),
 // :448-811 (chunk_stats + chunk_reduce, chunk = 32 tokens) and :868-1035
@@ -30,42 +31,87 @@ struct AttnParams {
   const int* position;  // seq = *position + 1
   int nh, nkv, max_ctx, window;
   int nsplit;
-  float scale;
+  float scale;          // log2(e) / sqrt(head_dim): scores in base-2 units
   float* scratch;       // [nh][MAXS][2] m,l  then [nh][MAXS][hd] o
 };
 
-// Scratch layout (floats): [0, 64) reserved, then m,l [nh][MAXS][2], then
-// o [nh][MAXS][hd].
+// Scratch layout (floats): [0, 64) per-KV-head arrival counters (uint32,
+// zero between calls), then m,l [nh][MAXS][2], then o [nh][MAXS][hd].
 constexpr int kCounterSlots = 64;
 
+// Scores are kept in base-2 units (the query is pre-scaled by log2(e)), so
+// every softmax weight is one v_exp_f32: 2^(a - m), with 0 for a = -inf.
 __device__ __forceinline__ float safe_exp_diff(float a, float m) {
-  return (a == -INFINITY) ? 0.f : expf(a - m);
+  return (a == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(a - m);
 }
 
+// Sum over aligned groups of 8 or 16 lanes with DPP lane moves (no LDS
+// crossbar): xor 1, xor 2, then the half-row and row mirrors.  Every lane of
+// the group ends with the same value.
+template <int N>
+__device__ __forceinline__ float dpp_group_sum(float v) {
+  static_assert(N == 8 || N == 16, "group of 8 or 16 lanes");
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  if constexpr (N == 16)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+
+// Split geometry shared by all workgroups of a launch: the live length is
+// divided into at most `nsplit` chunks of whole workgroup steps (MINCHUNK
+// tokens), so short contexts use few splits and the merge stays small.
+struct SplitGeom {
+  int seq, start, chunk, active;
+};
+template <int MINCHUNK>
+__device__ __forceinline__ SplitGeom split_geom(const AttnParams& p) {
+  SplitGeom sg;
+  int seq = p.position ? (*p.position + 1) : p.seq_len;
+  if (seq > p.max_ctx) seq = p.max_ctx;
+  sg.seq = seq;
+  sg.start = (p.window > 0 && seq > p.window) ? seq - p.window : 0;
+  const int len = seq - sg.start;
+  int chunk = (len + p.nsplit - 1) / p.nsplit;
+  chunk = ((chunk + MINCHUNK - 1) / MINCHUNK) * MINCHUNK;
+  if (chunk < MINCHUNK) chunk = MINCHUNK;
+  sg.chunk = chunk;
+  sg.active = (len + chunk - 1) / chunk;
+  return sg;
+}
+
+// One workgroup per (KV head, split).  A token row of one head (head_dim
+// fp16) is read by LPK = head_dim/8 lanes with 128-bit loads; the NG token
+// groups of the workgroup take TB consecutive tokens each per step, and the
+// next step's K/V rows are in flight while the current step is consumed.
+// Scores use v_dot2_f32_f16 against a hi/lo fp16 split of the fp32 query
+// (~22-bit query precision); P.V uses fp32 accumulation.
+// With more than one split, each workgroup publishes (m, l, o) with
+// device-scope stores and bumps the KV head's arrival counter; the last
+// workgroup to arrive merges the splits in split order (deterministic) and
+// resets the counter.
 template <int HD, int G, bool QF32, bool OF32>
 __global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
   constexpr int LPK = HD / 8;               // lanes per K/V row: 16 B each
   constexpr int NG = kAttnBlock / LPK;      // token groups per workgroup
-  constexpr int GPW = kWave / LPK;          // token groups per wave
-  constexpr int TB = 2;                     // tokens per group per iteration
-  constexpr int CT = NG * TB;               // tokens per workgroup iteration
+  constexpr int TB = 4;                     // tokens per group per step
+  constexpr int CT = NG * TB;               // tokens per workgroup step
 
-  __shared__ float wm[kAttnWaves][G], wl[kAttnWaves][G];
-  __shared__ float wo[kAttnWaves][G][HD];
-  
+  constexpr int GB = G < 4 ? G : 4;     // heads merged per LDS pass
+  __shared__ float go[GB][NG][HD];      // per-group partial outputs
+  __shared__ float gm[GB][NG], gl[GB][NG], gw[GB][NG], gM[GB];
+  __shared__ float fm[kAttnBlock], fl[kAttnBlock];  // split-merge lane partials
+  __shared__ int is_last;
+
   const int kvh = blockIdx.x;
   const int split = blockIdx.y;
-  int seq = p.position ? (*p.position + 1) : p.seq_len;
-  if (seq > p.max_ctx) seq = p.max_ctx;
-  const int start = (p.window > 0 && seq > p.window) ? seq - p.window : 0;
-  const int len = seq - start;
-  int chunk = (len + p.nsplit - 1) / p.nsplit;
-  chunk = ((chunk + CT - 1) / CT) * CT;
-  if (chunk < CT) chunk = CT;
-  const int active = (len + chunk - 1) / chunk;
+  const SplitGeom geo = split_geom<CT>(p);
+  const int active = geo.active;
   if (split >= active) return;  // uniform per workgroup
-  const int t0 = start + split * chunk;
-  const int t1 = min(t0 + chunk, seq);
+  const int t0 = geo.start + split * geo.chunk;
+  const int t1 = min(t0 + geo.chunk, geo.seq);
+  const int nsteps = (t1 - t0 + CT - 1) / CT;
 
   const int tid = threadIdx.x;
   const int lane = tid & (kWave - 1);
@@ -75,14 +121,39 @@ __global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
   const int kvdim = p.nkv * HD;
   const size_t col = static_cast<size_t>(kvh) * HD + cb * 8;
 
-  float qv[G][8];
+  // ---- K/V rows of step `it` (clamped to t1 - 1: always in bounds)
+  auto load = [&](int it, u32x4 (&kk)[TB], u32x4 (&vv)[TB]) {
+#pragma unroll
+    for (int tb = 0; tb < TB; ++tb) {
+      const int t = min(t0 + it * CT + gid * TB + tb, t1 - 1);
+      const size_t row = static_cast<size_t>(t) * kvdim + col;
+      kk[tb] = *reinterpret_cast<const u32x4*>(p.k + row);
+      vv[tb] = *reinterpret_cast<const u32x4*>(p.v + row);
+    }
+  };
+  u32x4 ka[TB], va[TB], kb[TB], vb[TB];
+  load(0, ka, va);
+
+  // query: hi/lo fp16 pairs, pre-scaled
+  uint32_t qh[G][4], ql[G][4];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int qi = (kvh * G + g) * HD + cb * 8 + e;
-      const float v = QF32 ? static_cast<const float*>(p.q)[qi] : h2f(static_cast<const uint16_t*>(p.q)[qi]);
-      qv[g][e] = v * p.scale;
+    for (int e = 0; e < 4; ++e) {
+      const int qi = (kvh * G + g) * HD + cb * 8 + 2 * e;
+      float v0, v1;
+      if constexpr (QF32) {
+        v0 = static_cast<const float*>(p.q)[qi];
+        v1 = static_cast<const float*>(p.q)[qi + 1];
+      } else {
+        v0 = h2f(static_cast<const uint16_t*>(p.q)[qi]);
+        v1 = h2f(static_cast<const uint16_t*>(p.q)[qi + 1]);
+      }
+      v0 *= p.scale;
+      v1 *= p.scale;
+      const f16 h0 = static_cast<f16>(v0), h1 = static_cast<f16>(v1);
+      qh[g][e] = h2_bits(h0, h1);
+      ql[g][e] = h2_bits(static_cast<f16>(v0 - static_cast<float>(h0)), static_cast<f16>(v1 - static_cast<float>(h1)));
     }
   float m[G], l[G], o[G][8];
 #pragma unroll
@@ -93,44 +164,27 @@ __global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
     for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
   }
 
-  for (int base = t0 + gid * TB; base < t1; base += CT) {
-    float kf[TB][8], vf[TB][8];
+  auto consume = [&](int it, const u32x4 (&kk)[TB], const u32x4 (&vv)[TB]) {
     bool valid[TB];
 #pragma unroll
-    for (int tb = 0; tb < TB; ++tb) {
-      const int t = base + tb;
-      valid[tb] = t < t1;
-      const size_t row = static_cast<size_t>(valid[tb] ? t : t1 - 1) * kvdim + col;
-      const u32x4 kw = *reinterpret_cast<const u32x4*>(p.k + row);
-      const u32x4 vw = *reinterpret_cast<const u32x4*>(p.v + row);
-      const uint32_t kd[4] = {kw.x, kw.y, kw.z, kw.w};
-      const uint32_t vd[4] = {vw.x, vw.y, vw.z, vw.w};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const f16x2 kh = as_h2(kd[e]);
-        const f16x2 vh = as_h2(vd[e]);
-        kf[tb][2 * e] = static_cast<float>(kh.x);
-        kf[tb][2 * e + 1] = static_cast<float>(kh.y);
-        vf[tb][2 * e] = static_cast<float>(vh.x);
-        vf[tb][2 * e + 1] = static_cast<float>(vh.y);
-      }
-    }
+    for (int tb = 0; tb < TB; ++tb) valid[tb] = t0 + it * CT + gid * TB + tb < t1;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float sc[TB];
 #pragma unroll
       for (int tb = 0; tb < TB; ++tb) {
+        const uint32_t kd[4] = {kk[tb].x, kk[tb].y, kk[tb].z, kk[tb].w};
         float d = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(qv[g][e], kf[tb][e], d);
-        d = group_sum<LPK>(d);
+        for (int e = 0; e < 4; ++e) d = dot2(kd[e], ql[g][e], dot2(kd[e], qh[g][e], d));
+        d = dpp_group_sum<LPK>(d);
         sc[tb] = valid[tb] ? d : -INFINITY;
       }
       float mx = sc[0];
 #pragma unroll
       for (int tb = 1; tb < TB; ++tb) mx = fmaxf(mx, sc[tb]);
       const float m_new = fmaxf(m[g], mx);
-      if (m_new == -INFINITY) continue;  // no token seen yet by this group
+      if (m_new == -INFINITY) continue;  // nothing valid seen yet by this group
       const float a = safe_exp_diff(m[g], m_new);
       float pw[TB];
       float ps = 0.f;
@@ -142,141 +196,174 @@ __global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
       l[g] = l[g] * a + ps;
       m[g] = m_new;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float acc = o[g][e] * a;
+      for (int e = 0; e < 8; ++e) o[g][e] *= a;
 #pragma unroll
-        for (int tb = 0; tb < TB; ++tb) acc = fmaf(pw[tb], vf[tb][e], acc);
-        o[g][e] = acc;
+      for (int tb = 0; tb < TB; ++tb) {
+        const uint32_t vd[4] = {vv[tb].x, vv[tb].y, vv[tb].z, vv[tb].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const f16x2 h = as_h2(vd[e]);
+          o[g][2 * e] = fmaf(static_cast<float>(h.x), pw[tb], o[g][2 * e]);
+          o[g][2 * e + 1] = fmaf(static_cast<float>(h.y), pw[tb], o[g][2 * e + 1]);
+        }
       }
     }
+  };
+
+  for (int it = 0; it < nsteps; it += 2) {
+    load(it + 1, kb, vb);
+    consume(it, ka, va);
+    if (it + 1 >= nsteps) break;
+    load(it + 2, ka, va);
+    consume(it + 1, kb, vb);
   }
 
-  // ---- merge the token groups of this wave (shuffles over the group bits)
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float M = m[g];
-#pragma unroll
-    for (int off = LPK; off < kWave; off <<= 1) M = fmaxf(M, __shfl_xor(M, off, kWave));
-    const float sc = (M == -INFINITY) ? 0.f : safe_exp_diff(m[g], M);
-    float lv = l[g] * sc;
-#pragma unroll
-    for (int off = LPK; off < kWave; off <<= 1) lv += __shfl_xor(lv, off, kWave);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float v = o[g][e] * sc;
-#pragma unroll
-      for (int off = LPK; off < kWave; off <<= 1) v += __shfl_xor(v, off, kWave);
-      o[g][e] = v;
-    }
-    if (lane < LPK) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) wo[wave][g][cb * 8 + e] = o[g][e];
-      if (lane == 0) {
-        wm[wave][g] = M;
-        wl[wave][g] = lv;
-      }
-    }
-  }
-  (void)GPW;
-  __syncthreads();
-
-  // ---- merge the waves; either finish (single split) or publish a partial
+  // ---- merge the token groups through LDS, GB heads per pass:
+  //   M = max m_grp,  w_grp = e^(m_grp - M),  L = sum l_grp w_grp,  o = sum o_grp w_grp.
   const size_t maxs = CPI_ATTN_MAX_SPLITS;
   float* ml = p.scratch + kCounterSlots;
   float* os = ml + static_cast<size_t>(p.nh) * maxs * 2;
-  for (int i = tid; i < G * HD; i += kAttnBlock) {
-    const int g = i / HD, d = i % HD;
-    float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][g]);
-    float L = 0.f, acc = 0.f;
+  for (int gb = 0; gb < G; gb += GB) {
 #pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
-      const float sc = safe_exp_diff(wm[w][g], M);
-      L = fmaf(wl[w][g], sc, L);
-      acc = fmaf(wo[w][g][d], sc, acc);
-    }
-    const int h = kvh * G + g;
-    if (active == 1) {
-      const float r = acc / L;
-      if (OF32) static_cast<float*>(p.out)[h * HD + d] = r;
-      else static_cast<uint16_t*>(p.out)[h * HD + d] = f2h(r);
-    } else {
-      os[(static_cast<size_t>(h) * maxs + split) * HD + d] = acc;
-      if (d == 0) {
-        ml[(static_cast<size_t>(h) * maxs + split) * 2 + 0] = M;
-        ml[(static_cast<size_t>(h) * maxs + split) * 2 + 1] = L;
+    for (int b = 0; b < GB; ++b) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) go[b][gid][cb * 8 + e] = o[gb + b][e];
+      if (cb == 0) {
+        gm[b][gid] = m[gb + b];
+        gl[b][gid] = l[gb + b];
       }
     }
+    lds_barrier();
+    if (tid < GB * NG) {
+      const int b = tid / NG, q = tid % NG;
+      float M = -INFINITY;
+#pragma unroll
+      for (int k2 = 0; k2 < NG; ++k2) M = fmaxf(M, gm[b][k2]);
+      gw[b][q] = safe_exp_diff(gm[b][q], M);
+      if (q == 0) gM[b] = M;
+    }
+    lds_barrier();
+    for (int i = tid; i < GB * HD; i += kAttnBlock) {
+      const int b = i / HD, d = i % HD;
+      float L = 0.f, acc = 0.f;
+#pragma unroll
+      for (int q = 0; q < NG; ++q) {
+        const float w = gw[b][q];
+        L = fmaf(gl[b][q], w, L);
+        acc = fmaf(go[b][q][d], w, acc);
+      }
+      const int h = kvh * G + gb + b;
+      if (active == 1) {
+        const float r = acc / L;
+        if (OF32) static_cast<float*>(p.out)[h * HD + d] = r;
+        else static_cast<uint16_t*>(p.out)[h * HD + d] = f2h(r);
+      } else {
+        const size_t slot = static_cast<size_t>(h) * maxs + split;
+        __hip_atomic_store(&os[slot * HD + d], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) {
+          __hip_atomic_store(&ml[slot * 2 + 0], gM[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(&ml[slot * 2 + 1], L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+    lds_barrier();  // go / gm / gl / gw are reused by the next pass
   }
-}
+  if (active == 1) return;
 
-// Merge the split partials of one query head (fixed order):
-//   M = max m_s,  L = sum l_s e^(m_s - M),  out = sum o_s e^(m_s - M) / L.
-// One workgroup per head; the split axis is spread over the threads so the
-// loads are independent.
-template <int HD, bool OF32>
-__global__ void __launch_bounds__(kAttnBlock) attn_merge_kernel(AttnParams p) {
-  constexpr int SUB = kAttnBlock / HD * 4;  // split lanes per column (4 columns per thread)
-  __shared__ float wsh[CPI_ATTN_MAX_SPLITS];
-  __shared__ float red[kAttnWaves];
-  __shared__ float part[SUB][HD];
-  const int h = blockIdx.x;
-  int seq = p.position ? (*p.position + 1) : p.seq_len;
-  if (seq > p.max_ctx) seq = p.max_ctx;
-  const int start = (p.window > 0 && seq > p.window) ? seq - p.window : 0;
-  const int len = seq - start;
-  constexpr int CT = (kAttnBlock / (HD / 8)) * 2;
-  int chunk = (len + p.nsplit - 1) / p.nsplit;
-  chunk = ((chunk + CT - 1) / CT) * CT;
-  if (chunk < CT) chunk = CT;
-  const int active = (len + chunk - 1) / chunk;
-  if (active <= 1) return;  // the split kernel already wrote the output
-  const size_t maxs = CPI_ATTN_MAX_SPLITS;
-  const float* ml = p.scratch + kCounterSlots + static_cast<size_t>(h) * maxs * 2;
-  const float* os = p.scratch + kCounterSlots + static_cast<size_t>(p.nh) * maxs * 2 +
-                    static_cast<size_t>(h) * maxs * HD;
-  const int tid = threadIdx.x;
-  float mv = -INFINITY;
-  if (tid < active) mv = ml[2 * tid];
-  // block max of m
-  float M = wave_max(mv);
-  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = M;
+  // ---- arrival: the partial stores above are device-coherent (write-through);
+  // waiting for their completion before the counter update orders them
+  // before it without an L2 writeback.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  M = red[0];
-#pragma unroll
-  for (int w = 1; w < kAttnWaves; ++w) M = fmaxf(M, red[w]);
-  __syncthreads();
-  float lw = 0.f;
-  if (tid < active) {
-    const float w = safe_exp_diff(mv, M);
-    wsh[tid] = w;
-    lw = ml[2 * tid + 1] * w;
+  unsigned* cnt = reinterpret_cast<unsigned*>(p.scratch) + kvh;
+  if (tid == 0) {
+    const unsigned prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == static_cast<unsigned>(active - 1);
   }
-  const float L = block_sum(lw, red);  // includes a barrier: wsh is visible
-  // columns: thread handles 4 consecutive columns for splits s = sub, sub+SUB, ...
-  const int c4 = (tid % (HD / 4)) * 4;
-  const int sub = tid / (HD / 4);
-  float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int s2 = sub; s2 < active; s2 += SUB) {
-    const float w = wsh[s2];
-    typedef float f32x4 __attribute__((ext_vector_type(4)));
-    const f32x4 v = *reinterpret_cast<const f32x4*>(os + static_cast<size_t>(s2) * HD + c4);
-    acc[0] = fmaf(v.x, w, acc[0]);
-    acc[1] = fmaf(v.y, w, acc[1]);
-    acc[2] = fmaf(v.z, w, acc[2]);
-    acc[3] = fmaf(v.w, w, acc[3]);
-  }
-#pragma unroll
-  for (int e = 0; e < 4; ++e) part[sub][c4 + e] = acc[e];
   __syncthreads();
-  if (tid < HD) {
-    float r = 0.f;
+  if (!is_last) return;
+  if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+  // ---- last arrival merges the splits of all G heads at once.  Thread t
+  // serves head t / TPH, CPT columns and the splits s = sub + SUB*j; all of a
+  // round's loads are issued before any is consumed.  Each thread keeps an
+  // online (max, sum) over its splits; the SUB lanes of a column are combined
+  // in a fixed order, so the result does not depend on arrival order.
+  constexpr int TPH = kAttnBlock / G;             // threads per head
+  constexpr int CPT = HD > TPH ? HD / TPH : 1;    // columns per thread
+  constexpr int SUB = TPH > HD ? TPH / HD : 1;    // split lanes per column
+  constexpr int MAXJ = CPT <= 2 ? 16 : 8;
+  auto ld = [](const float* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  const int g = tid / TPH;
+  const int r = tid % TPH;
+  const int h = kvh * G + g;
+  const int c0 = (r % (HD / CPT)) * CPT;  // first column
+  const int sub = r / (HD / CPT);
+  const float* mlh = ml + static_cast<size_t>(h) * maxs * 2;
+  const float* osh = os + static_cast<size_t>(h) * maxs * HD;
+  float Mt = -INFINITY, Lt = 0.f, acc[CPT];
 #pragma unroll
-    for (int q = 0; q < SUB; ++q) r += part[q][tid];
-    r /= L;
-    if (OF32) static_cast<float*>(p.out)[h * HD + tid] = r;
-    else static_cast<uint16_t*>(p.out)[h * HD + tid] = f2h(r);
+  for (int c = 0; c < CPT; ++c) acc[c] = 0.f;
+  for (int s0 = 0; s0 < active; s0 += SUB * MAXJ) {
+    float mv[MAXJ], lv[MAXJ], ov[MAXJ][CPT];
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+      const int s2 = min(s0 + sub + SUB * j, active - 1);
+      mv[j] = ld(&mlh[2 * s2]);
+      lv[j] = ld(&mlh[2 * s2 + 1]);
+#pragma unroll
+      for (int c = 0; c < CPT; ++c) ov[j][c] = ld(&osh[static_cast<size_t>(s2) * HD + c0 + c]);
+    }
+    float Mr = Mt;
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j)
+      if (s0 + sub + SUB * j < active) Mr = fmaxf(Mr, mv[j]);
+    const float a = safe_exp_diff(Mt, Mr);
+    Lt *= a;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) acc[c] *= a;
+#pragma unroll
+    for (int j = 0; j < MAXJ; ++j) {
+      if (s0 + sub + SUB * j < active) {
+        const float w = safe_exp_diff(mv[j], Mr);
+        Lt = fmaf(lv[j], w, Lt);
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) acc[c] = fmaf(ov[j][c], w, acc[c]);
+      }
+    }
+    Mt = Mr;
+  }
+  if constexpr (SUB == 1) {
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+      const float res = acc[c] / Lt;
+      if (OF32) static_cast<float*>(p.out)[h * HD + c0 + c] = res;
+      else static_cast<uint16_t*>(p.out)[h * HD + c0 + c] = f2h(res);
+    }
+  } else {
+    // combine the SUB split lanes of each column (CPT == 1 here)
+    fm[tid] = Mt;
+    fl[tid] = Lt;
+    float* fo = &go[0][0][0];  // go is free: reused as [kAttnBlock] scratch
+    static_assert(GB * NG * HD >= kAttnBlock, "scratch reuse");
+    fo[tid] = acc[0];
+    lds_barrier();
+    if (sub == 0) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < SUB; ++q) M = fmaxf(M, fm[tid + q * HD]);
+      float L = 0.f, o2 = 0.f;
+#pragma unroll
+      for (int q = 0; q < SUB; ++q) {
+        const float w = safe_exp_diff(fm[tid + q * HD], M);
+        L = fmaf(fl[tid + q * HD], w, L);
+        o2 = fmaf(fo[tid + q * HD], w, o2);
+      }
+      const float res = o2 / L;
+      if (OF32) static_cast<float*>(p.out)[h * HD + c0] = res;
+      else static_cast<uint16_t*>(p.out)[h * HD + c0] = f2h(res);
+    }
   }
 }
 
@@ -289,10 +376,6 @@ hipError_t launch_g(const AttnParams& p, bool qf32, bool of32, hipStream_t s) {
   else if (qf32) hipLaunchKernelGGL((attn_kernel<HD, G, true, false>), grid, dim3(kAttnBlock), 0, s, p);
   else if (of32) hipLaunchKernelGGL((attn_kernel<HD, G, false, true>), grid, dim3(kAttnBlock), 0, s, p);
   else hipLaunchKernelGGL((attn_kernel<HD, G, false, false>), grid, dim3(kAttnBlock), 0, s, p);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (of32) hipLaunchKernelGGL((attn_merge_kernel<HD, true>), dim3(p.nh), dim3(kAttnBlock), 0, s, p);
-  else hipLaunchKernelGGL((attn_merge_kernel<HD, false>), dim3(p.nh), dim3(kAttnBlock), 0, s, p);
   return hipGetLastError();
 }
 
@@ -332,7 +415,7 @@ hipError_t attn_launch(const void* q, bool qf32, const uint16_t* k, const uint16
   p.seq_len = seq_len; p.position = position;
   p.nh = nh; p.nkv = nkv; p.max_ctx = max_ctx; p.window = window;
   p.nsplit = attn_num_splits(nkv);
-  p.scale = 1.f / sqrtf(static_cast<float>(hd));
+  p.scale = 1.4426950408889634f / sqrtf(static_cast<float>(hd));  // log2(e) / sqrt(hd)
   p.scratch = scratch;
   const int G = nh / nkv;
   if (hd == 64) return launch_hd<64>(p, G, qf32, of32, s);

@@ -32,6 +32,14 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2(as_h2(a), as_h2(b), c, false);
 }
 
+// Workgroup barrier that only orders LDS: waits for this wave's LDS operations
+// (lgkmcnt) but leaves outstanding global loads in flight, unlike
+// __syncthreads(), whose fence drains them.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // vmcnt=63 (no wait), expcnt=7, lgkmcnt=0
+  __builtin_amdgcn_s_barrier();
+}
+
 // Butterfly sum over a power-of-two group of adjacent lanes.
 template <int WIDTH>
 __device__ __forceinline__ float group_sum(float v) {

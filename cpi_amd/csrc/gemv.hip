@@ -78,14 +78,6 @@ struct GemvParams {
 
 enum { EPI_DUAL_F16 = 100 };
 
-// Workgroup barrier that only orders LDS: waits for this wave's LDS operations
-// (lgkmcnt) but leaves outstanding global loads in flight, unlike
-// __syncthreads(), whose fence drains them.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // vmcnt=63 (no wait), expcnt=7, lgkmcnt=0
-  __builtin_amdgcn_s_barrier();
-}
-
 // ---------------------------------------------------------------------------
 // Activation preparation (one chunk).
 // ---------------------------------------------------------------------------

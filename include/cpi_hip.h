@@ -153,8 +153,10 @@ int cpi_hip_gather_rows(const void* src, void* dst, const int* idx, int rows,
  * Decode attention (exact online softmax, split-K over context, GQA).
  * q fp32 or fp16 [num_heads*head_dim] (q_is_f32), caches fp16
  * [max_ctx, num_kv_heads*head_dim], out fp32 or fp16 [num_heads*head_dim].
- * Scratch: cpi_hip_attention_scratch_floats() floats (split partials);
- * calls sharing one scratch buffer must not overlap.
+ * Scratch: cpi_hip_attention_scratch_floats() floats (split partials and
+ * per-KV-head arrival counters).  Zero-fill it once before first use; every
+ * call leaves the counters at zero again.  Calls sharing one scratch buffer
+ * must not overlap.
  * Replaces launch_attention_step / _device_pos (kernels.cuh:216-275):
  * chunk_stats + chunk_reduce, gqa_decode_kernel and the tiled kernel.
  * ---------------------------------------------------------------------- */

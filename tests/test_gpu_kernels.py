@@ -222,6 +222,8 @@ def test_attention_parity(nh, nkv, hd, seq):
     ref16 = oracle.attention(q.astype(np.float16).astype(np.float32), kc[:seq].astype(np.float32),
                              vc[:seq].astype(np.float32), seq, nh, nkv, hd)
     np.testing.assert_allclose(G.host(out16, np.float16, nh * hd).astype(np.float32), ref16, atol=2e-3)
+    # the per-KV-head arrival counters are back at zero for the next call
+    assert not G.host(scratch, np.uint32, 64).any()
 
 
 def test_attention_sliding_window():
