@@ -70,6 +70,20 @@ def cpu_baseline(path: str, seconds: float = 15.0):
                       f"{dt:.1f}s wall, OMP threads={cores}"}
 
 
+def profiled_traffic():
+    """HBM bytes per launch of the w1|w3 GEMV, from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary committed under profiles/ (calibrated against a plain
+    copy there); None when the summary is absent."""
+    p = os.path.join(ROOT, "profiles", "gemv_w13_i4g32_traffic.md")
+    try:
+        for line in open(p):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -118,8 +132,9 @@ def main():
         gemv[name] = {"us": round(r["us"], 3), "gbps": round(r["gbps"], 1), "bytes": r["bytes"]}
         log(f"[bench] gemv {name} {R}x{K}: {r['us']:.2f} us, {r['gbps']:.0f} GB/s")
     dom = gemv["w13"]
+    traffic = profiled_traffic()
     roof = {"bound": "hbm", "achieved": dom["gbps"], "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-            "frac": round(dom["gbps"] / PEAK_HBM_GBPS, 4), "traffic": None,
+            "frac": round(dom["gbps"] / PEAK_HBM_GBPS, 4), "traffic": traffic,
             "kernel": "gemv_kernel<I4G32> w1|w3 22016x4096", "bytes_per_launch": dom["bytes"],
             "us_per_launch": dom["us"]}
 

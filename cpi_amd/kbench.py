@@ -134,9 +134,44 @@ def time_attention(nh, nkv, hd, ctx, iters=100, rotate_bytes=2 << 30):
     return {"ctx": ctx, "us": us, "bytes": nbytes, "gbps": nbytes / us / 1e3}
 
 
+def pmc_workload(copy_mib: int = 512, launches: int = 20):
+    """Eager launches for `rocprofv3 --pmc` runs (counters are read per
+    dispatch): `launches` plain device-to-device copies of `copy_mib` MiB (the
+    calibration kernel: it moves exactly 2 x copy_mib MiB), then `launches`
+    w1|w3 int4-g32 GEMVs (22016 x 4096) over distinct weight copies."""
+    src = torch.empty(copy_mib << 20, dtype=torch.uint8, device="cuda").random_(0, 256)
+    dst = torch.empty_like(src)
+    for _ in range(launches):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    R, K = 22016, 4096
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(K, device="cuda", generator=gen).half()
+    y = torch.empty(R, device="cuda", dtype=torch.float16)
+    fn = _lib.lib().cpi_hip_gemv
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for i in range(launches):
+        w, s, sc = _weights("i4g32", R, K, gen)
+        d = _lib.GemvDesc()
+        d.wfmt, d.w, d.scales, d.scale_count = _lib.W_I4G32, w.data_ptr(), s.data_ptr(), sc
+        d.out_features, d.in_features, d.x, d.x_is_f32 = R, K, x.data_ptr(), 0
+        d.epilogue, d.y = _lib.EPI_STORE_F16, y.data_ptr()
+        torch.cuda.synchronize()
+        rc = fn(ctypes.byref(d), st)
+        if rc:
+            raise _lib.CpiHipError(_lib.lib().cpi_hip_last_error_string().decode())
+        torch.cuda.synchronize()
+        del w, s
+    print(f"[kbench] pmc workload: {launches} copies of {copy_mib} MiB, {launches} w13 GEMVs", flush=True)
+
+
 if __name__ == "__main__":
     import json
     import sys
+    if sys.argv[1:2] == ["pmc"]:
+        pmc_workload()
+        sys.exit(0)
     fmts = sys.argv[1:] or ["i4g32", "i4", "i8", "f16"]
     for f in fmts:
         for name, R, K in GEMV_SHAPES:
