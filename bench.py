@@ -150,7 +150,7 @@ def main():
         "vs_baseline": None, "dtype": "int4-g32 weights, fp16 act/KV, fp32 accumulate", "data": "synthetic",
         "config": {"workload": "llama2-7b-int4g32-decode", "layers": args.layers, "hidden": 4096,
                    "heads": 32, "intermediate": 11008, "vocab": 32000, "prompt_tokens": PROMPT_LEN,
-                   "decode_tokens": DECODE_LEN, "prefill": "sequential (graph-captured decode steps)",
+                   "decode_tokens": DECODE_LEN, "prefill": "chunked MFMA (128 tokens per chunk)",
                    "parallelism": "single-gpu"},
         "prefill_tok_per_s": round(args.steps * (PROMPT_LEN - 1) / (prefill_ms / 1e3), 1),
         "gemv_i4g32": gemv,

@@ -31,6 +31,18 @@ class GemvDesc(ctypes.Structure):
     ]
 
 
+class GemmDesc(ctypes.Structure):
+    """Mirror of cpi_gemm_desc."""
+    _fields_ = [
+        ("wfmt", c_int), ("w", c_void_p), ("scales", c_void_p), ("scale_count", c_int),
+        ("out_features", c_int), ("in_features", c_int), ("x", c_void_p), ("num_tokens", c_int),
+        ("epilogue", c_int), ("y", c_void_p),
+        ("num_heads", c_int), ("num_kv_heads", c_int), ("head_dim", c_int), ("start_position", c_int),
+        ("rope_cos", c_void_p), ("rope_sin", c_void_p), ("k_cache", c_void_p), ("v_cache", c_void_p),
+        ("max_context", c_int),
+    ]
+
+
 W_F16, W_I8ROW, W_I4ROW, W_I4G32 = 0, 1, 2, 3
 EPI_STORE_F32, EPI_STORE_F16, EPI_RESID_ADD, EPI_SWIGLU, EPI_QKV_ROPE = 0, 1, 2, 3, 4
 ATTN_MAX_SPLITS = 256
@@ -56,6 +68,9 @@ _SIGS = {
     "cpi_hip_attention_step": (c_int, [c_void_p] * 4 + [c_int] * 4 + [c_void_p, c_void_p]),
     "cpi_hip_attention_step_device_pos": (c_int, [c_void_p] * 5 + [c_int] * 4 + [c_void_p, c_void_p]),
     "cpi_hip_attention_prefill": (c_int, [c_void_p] * 4 + [c_int] * 5 + [c_void_p]),
+    "cpi_hip_attention_prefill_window": (c_int, [c_void_p] * 4 + [c_int] * 6 + [c_void_p]),
+    "cpi_hip_prefill_gemm": (c_int, [ctypes.POINTER(GemmDesc), c_void_p]),
+    "cpi_hip_rmsnorm_rows_f32": (c_int, [c_void_p] * 3 + [c_int, c_int, c_float, c_void_p]),
     "cpi_hip_rmsnorm": (c_int, [c_void_p] * 3 + [c_int, c_int, c_float, c_void_p]),
     "cpi_hip_embedding_lookup": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p]),
     "cpi_hip_embedding_lookup_f32": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p]),

@@ -12,6 +12,7 @@
 #include "gemv.hip"
 #include "attention.hip"
 #include "ops.hip"
+#include "prefill.hip"
 
 namespace {
 
@@ -396,9 +397,86 @@ int cpi_hip_dequant_rowwise_int8_to_fp16(const int8_t* src, const float* sc, uin
   return check(hipGetLastError(), "dequant_rowwise");
 }
 
-int cpi_hip_attention_prefill(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int,
-                              int, int, int, int, cpi_stream_t) {
-  return fail("attention_prefill: not built yet");
+int cpi_hip_attention_prefill_window(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out,
+                                     int n, int start, int nh, int nkv, int hd, int window, cpi_stream_t s) {
+  if (!q || !k || !v || !out) return fail("attention_prefill: null pointer");
+  if (n <= 0) return 0;
+  if (start < 0 || nh <= 0 || nkv <= 0 || nh % nkv != 0) return fail("attention_prefill: bad head counts");
+  if (hd != 64 && hd != 128) return fail("attention_prefill: head_dim must be 64 or 128");
+  if (((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) | reinterpret_cast<uintptr_t>(v)) & 15) != 0)
+    return fail("attention_prefill: q and caches must be 16-byte aligned");
+  cpi::APParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.out = out;
+  p.M = n;
+  p.start = start;
+  p.nh = nh;
+  p.nkv = nkv;
+  p.window = window;
+  p.scale_log2 = 1.4426950408889634f / sqrtf(static_cast<float>(hd));
+  return check(cpi::attn_prefill_launch(p, hd, S(s)), "attention_prefill");
+}
+
+int cpi_hip_attention_prefill(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* out, int n,
+                              int start, int nh, int nkv, int hd, cpi_stream_t s) {
+  return cpi_hip_attention_prefill_window(q, k, v, out, n, start, nh, nkv, hd, 0, s);
+}
+
+int cpi_hip_prefill_gemm(const cpi_gemm_desc* d, cpi_stream_t s) {
+  if (!d) return fail("prefill_gemm: null descriptor");
+  if (cpi::gemv_elems_per_chunk(d->wfmt) == 0) return fail("prefill_gemm: unknown weight format");
+  if (!d->w || !d->x || !d->y || d->out_features <= 0 || d->in_features <= 0)
+    return fail("prefill_gemm: null pointer or empty shape");
+  if (d->num_tokens <= 0) return 0;
+  if (d->in_features % 64 != 0) return fail("prefill_gemm: in_features must be a multiple of 64");
+  if (((reinterpret_cast<uintptr_t>(d->w) | reinterpret_cast<uintptr_t>(d->x)) & 15) != 0)
+    return fail("prefill_gemm: weights and x must be 16-byte aligned");
+  if (d->wfmt != CPI_W_F16 && !d->scales) return fail("prefill_gemm: missing scales");
+  if ((d->wfmt == CPI_W_I8ROW || d->wfmt == CPI_W_I4ROW) && d->scale_count != 1 &&
+      d->scale_count != d->out_features)
+    return fail("prefill_gemm: scale_count must be 1 or out_features");
+  if (d->epilogue < CPI_EPI_STORE_F32 || d->epilogue > CPI_EPI_QKV_ROPE) return fail("prefill_gemm: unknown epilogue");
+  if (d->epilogue == CPI_EPI_SWIGLU && d->out_features % 8 != 0)
+    return fail("prefill_gemm: SWIGLU needs out_features % 8 == 0");
+  cpi::PGemmParams p{};
+  p.w = static_cast<const uint8_t*>(d->w);
+  p.scales = d->scales;
+  p.scale_count = d->scale_count;
+  p.N = d->out_features;
+  p.K = d->in_features;
+  p.M = d->num_tokens;
+  p.x = d->x;
+  p.epi = d->epilogue;
+  p.y = d->y;
+  if (d->epilogue == CPI_EPI_QKV_ROPE) {
+    if (d->head_dim % 8 != 0 || d->num_heads <= 0 || d->num_kv_heads <= 0)
+      return fail("prefill_gemm: QKV_ROPE needs head_dim % 8 == 0 and positive head counts");
+    if (d->out_features != (d->num_heads + 2 * d->num_kv_heads) * d->head_dim)
+      return fail("prefill_gemm: QKV_ROPE out_features != (nh + 2 nkv) * head_dim");
+    if (!d->rope_cos || !d->rope_sin || !d->k_cache || !d->v_cache)
+      return fail("prefill_gemm: QKV_ROPE needs rope tables and KV cache");
+    if (d->start_position < 0 || d->start_position + d->num_tokens > d->max_context)
+      return fail("prefill_gemm: chunk positions exceed max_context");
+    p.nh = d->num_heads;
+    p.nkv = d->num_kv_heads;
+    p.hd = d->head_dim;
+    p.start = d->start_position;
+    p.rope_cos = d->rope_cos;
+    p.rope_sin = d->rope_sin;
+    p.k_cache = d->k_cache;
+    p.v_cache = d->v_cache;
+    p.max_ctx = d->max_context;
+  }
+  return check(cpi::pgemm_launch(d->wfmt, p, S(s)), "prefill_gemm");
+}
+
+int cpi_hip_rmsnorm_rows_f32(const float* x, const uint16_t* w, uint16_t* y, int rows, int cols, float eps,
+                             cpi_stream_t s) {
+  if (!x || !w || !y || cols <= 0) return fail("rmsnorm_rows_f32: null pointer or empty shape");
+  if (rows <= 0) return 0;
+  return check(cpi::rmsnorm_rows_launch(x, w, y, rows, cols, eps, S(s)), "rmsnorm_rows_f32");
 }
 
 }  // extern "C"

@@ -33,6 +33,7 @@ void cpi_engine_default_options(cpi_engine_options* o) {
   o->verbose = d.verbose ? 1 : 0;
   o->profile_decode_phases = 0;
   o->graph_steps = d.graph_steps;
+  o->prefill_chunk = d.prefill_chunk;
 }
 
 const char* cpi_engine_last_error(void) { return g_err.c_str(); }
@@ -56,6 +57,7 @@ cpi_engine* cpi_engine_create(const cpi_engine_options* o) {
     opt.verbose = o->verbose != 0;
     opt.profile_decode_phases = o->profile_decode_phases != 0;
     opt.graph_steps = o->graph_steps;
+    opt.prefill_chunk = o->prefill_chunk;
     e->eng.initialize(opt);
   } catch (const std::exception& ex) {
     fail(ex);

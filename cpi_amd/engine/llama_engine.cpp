@@ -12,6 +12,7 @@
 #include <algorithm>
 #include <chrono>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <iostream>
 #include <numeric>
@@ -298,6 +299,27 @@ void LlamaEngine::initialize(const EngineOptions& options) {
   HIP_OK(hipMemset(d_token_, 0, 4));
   HIP_OK(hipMemset(d_pos_, 0, 4));
   HIP_OK(hipMemset(d_step_, 0, 4));
+  // ---- chunked prefill: MFMA GEMMs need every GEMM K to be a multiple of 64
+  // and the prefill attention head_dim 64 or 128; otherwise prompts run
+  // token by token through the decode graphs.
+  {
+    int chunk = opts_.prefill_chunk;
+    if (chunk <= 0) {
+      chunk = 128;
+      if (const char* env = std::getenv("LLAMA_INFER_PREFILL_CHUNK_SIZE")) chunk = std::max(1, std::atoi(env));
+    }
+    chunk = std::min(chunk, opts_.max_context);
+    const bool shapes_ok = H % 64 == 0 && q_dim_ % 64 == 0 && I % 64 == 0 && (head_dim_ == 64 || head_dim_ == 128);
+    prefill_chunk_ = shapes_ok ? chunk : 1;
+    if (prefill_chunk_ > 1) {
+      const std::size_t C = static_cast<std::size_t>(prefill_chunk_);
+      px_ = static_cast<float*>(dmalloc(C * H * 4));
+      pxn_ = static_cast<uint16_t*>(dmalloc(C * H * 2));
+      pq_ = static_cast<uint16_t*>(dmalloc(C * q_dim_ * 2));
+      patt_ = static_cast<uint16_t*>(dmalloc(C * q_dim_ * 2));
+      pff_ = static_cast<uint16_t*>(dmalloc(C * I * 2));
+    }
+  }
   HIP_OK(hipDeviceSynchronize());
 
   build_graphs();
@@ -305,6 +327,7 @@ void LlamaEngine::initialize(const EngineOptions& options) {
     std::cout << "[engine] resident gfx950 decode: layers=" << NL << " hidden=" << H << " heads=" << NH
               << " kv_heads=" << NKV << " head_dim=" << head_dim_ << " inter=" << I << " vocab=" << V
               << " max_context=" << opts_.max_context << " rope_theta=" << theta_
+              << " prefill_chunk=" << prefill_chunk_
               << " weights_mb=" << (weight_bytes_ >> 20) << "\n";
     std::cout << "[startup] phase=initialize ms=" << ms_since(t0) << "\n";
   }
@@ -361,6 +384,47 @@ void LlamaEngine::enqueue_step(bool with_head) {
   }
 }
 
+// Prompt positions [0, n_pre) in chunks of prefill_chunk_ tokens: per layer
+// RMSNorm rows -> QKV GEMM (+RoPE, KV store) -> causal prefill attention ->
+// o_proj GEMM (+residual) -> RMSNorm rows -> w1|w3 GEMM (+SwiGLU) -> w2 GEMM
+// (+residual), the order of prefill_prompt (llama_engine_generation.cpp:71-454).
+// No logits are produced; the first decode step consumes prompt[n_pre].
+void LlamaEngine::prefill_chunked(const std::vector<int>& prompt, int n_pre) {
+  const int H = cfg_.hidden_size;
+  auto gemm = [&](const Linear& L, const uint16_t* x, int rows, int epi, void* y) {
+    cpi_gemm_desc d{};
+    d.wfmt = L.wfmt; d.w = L.w; d.scales = L.scales; d.scale_count = L.scale_count;
+    d.out_features = L.rows; d.in_features = L.cols; d.x = x; d.num_tokens = rows;
+    d.epilogue = epi; d.y = y;
+    return d;
+  };
+  for (int c0 = 0; c0 < n_pre; c0 += prefill_chunk_) {
+    const int rows = std::min(prefill_chunk_, n_pre - c0);
+    CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_prompt_ + c0, px_, rows, H, stream_));
+    for (auto& L : layers_) {
+      CPI_OK(cpi_hip_rmsnorm_rows_f32(px_, L.norm_att, pxn_, rows, H, cfg_.norm_eps, stream_));
+      cpi_gemm_desc q = gemm(L.qkv, pxn_, rows, CPI_EPI_QKV_ROPE, pq_);
+      q.num_heads = cfg_.num_heads; q.num_kv_heads = cfg_.num_kv_heads; q.head_dim = head_dim_;
+      q.start_position = c0; q.rope_cos = rope_cos_; q.rope_sin = rope_sin_;
+      q.k_cache = L.k_cache; q.v_cache = L.v_cache; q.max_context = opts_.max_context;
+      CPI_OK(cpi_hip_prefill_gemm(&q, stream_));
+      CPI_OK(cpi_hip_attention_prefill_window(pq_, L.k_cache, L.v_cache, patt_, rows, c0, cfg_.num_heads,
+                                              cfg_.num_kv_heads, head_dim_, cfg_.sliding_window, stream_));
+      cpi_gemm_desc o = gemm(L.wo, patt_, rows, CPI_EPI_RESID_ADD, px_);
+      CPI_OK(cpi_hip_prefill_gemm(&o, stream_));
+      CPI_OK(cpi_hip_rmsnorm_rows_f32(px_, L.norm_ffn, pxn_, rows, H, cfg_.norm_eps, stream_));
+      cpi_gemm_desc g = gemm(L.w13, pxn_, rows, CPI_EPI_SWIGLU, pff_);
+      CPI_OK(cpi_hip_prefill_gemm(&g, stream_));
+      cpi_gemm_desc w = gemm(L.w2, pff_, rows, CPI_EPI_RESID_ADD, px_);
+      CPI_OK(cpi_hip_prefill_gemm(&w, stream_));
+    }
+  }
+  const int tok = prompt[static_cast<std::size_t>(n_pre)];
+  HIP_OK(hipMemcpyAsync(d_token_, &tok, 4, hipMemcpyHostToDevice, stream_));
+  HIP_OK(hipMemcpyAsync(d_pos_, &n_pre, 4, hipMemcpyHostToDevice, stream_));
+  HIP_OK(hipStreamSynchronize(stream_));
+}
+
 void LlamaEngine::build_graphs() {
   auto capture = [&](bool head, int steps) {
     hipGraph_t g = nullptr;
@@ -412,6 +476,10 @@ std::vector<int> LlamaEngine::generate_stream(const std::vector<int>& prompt_in,
   const auto tp = Clock::now();
   int pos = 0;
   const int n_pre = prompt.empty() ? 0 : static_cast<int>(prompt.size()) - 1;
+  if (prefill_chunk_ > 1 && n_pre > 0) {
+    prefill_chunked(prompt, n_pre);
+    pos = n_pre;
+  }
   while (pos < n_pre) {
     if (n_pre - pos >= graph_steps_) {
       run_graph(g_prefill_many_);

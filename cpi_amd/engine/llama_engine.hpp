@@ -56,6 +56,9 @@ struct EngineOptions {
   int tq_first_token_timeout_ms = 120000;
   int eos_token_id = 2;
   int graph_steps = 16;  // decode steps captured per graph launch (this engine)
+  // prompt tokens per chunked-prefill step; 0 = LLAMA_INFER_PREFILL_CHUNK_SIZE
+  // or 128, 1 = token-by-token (llama_engine.cpp:1077-1078)
+  int prefill_chunk = 0;
 };
 
 // engine::BenchmarkStats (llama_engine.hpp:102-127).
@@ -143,6 +146,7 @@ class LlamaEngine {
   uint16_t* upload_f16(const std::string& name, std::size_t expect_bytes);
 
   void enqueue_step(bool with_head);
+  void prefill_chunked(const std::vector<int>& prompt, int n_pre);
   void build_graphs();
   void run_graph(hipGraphExec_t g);
   void reset_state(const std::vector<int>& prompt);
@@ -174,6 +178,11 @@ class LlamaEngine {
   hipGraphExec_t g_decode_many_ = nullptr, g_decode_one_ = nullptr;
   hipGraphExec_t g_prefill_many_ = nullptr, g_prefill_one_ = nullptr;
   int graph_steps_ = 16;
+
+  // chunked prefill (MFMA GEMMs): residual [C, H] fp32, GEMM inputs fp16
+  int prefill_chunk_ = 1;
+  float* px_ = nullptr;
+  uint16_t *pxn_ = nullptr, *pq_ = nullptr, *patt_ = nullptr, *pff_ = nullptr;
 
   float* capture_ = nullptr;
   int capture_steps_ = 0;

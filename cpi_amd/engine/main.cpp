@@ -18,7 +18,7 @@ void usage(std::ostream& os) {
   os << "Usage: llama_infer <model.ll2c> --tokens csv [--max-new n] [--temp t] [--max-context n] "
         "[--top-k n] [--top-p p] [--repeat-penalty r] [--rope-theta f] [--eos-token n] [--no-loop-guard] "
         "[--benchmark] [--benchmark-reps n] [--benchmark-warmup n] [--benchmark-phases] [--runtime-metrics] "
-        "[--inspect-next-topk n] [--gpu-cache-all] [--no-resource-limits] [--graph-steps n] [--quiet]\n";
+        "[--inspect-next-topk n] [--gpu-cache-all] [--no-resource-limits] [--graph-steps n] [--prefill-chunk n] [--quiet]\n";
 }
 
 std::vector<int> parse_csv(const std::string& s) {
@@ -77,6 +77,7 @@ int main(int argc, char** argv) {
       else if (a == "--benchmark-phases" || a == "--runtime-metrics") phases = true;
       else if (a == "--inspect-next-topk") inspect_k = std::stoi(next());
       else if (a == "--graph-steps") opt.graph_steps = std::stoi(next());
+      else if (a == "--prefill-chunk") opt.prefill_chunk = std::stoi(next());
       else if (a == "--quiet") quiet = true;
       else if (a == "--gpu-cache-all" || a == "--no-resource-limits" || a == "--no-split-attention") {
         // always fully resident; no host guardrails on this path

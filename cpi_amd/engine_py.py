@@ -16,7 +16,8 @@ class Options(ctypes.Structure):
     _fields_ = [("model_path", ctypes.c_char_p), ("max_context", ctypes.c_int), ("rope_theta", ctypes.c_float),
                 ("eos_token_id", ctypes.c_int), ("loop_guard", ctypes.c_int), ("top_k", ctypes.c_int),
                 ("top_p", ctypes.c_float), ("repetition_penalty", ctypes.c_float), ("verbose", ctypes.c_int),
-                ("profile_decode_phases", ctypes.c_int), ("graph_steps", ctypes.c_int)]
+                ("profile_decode_phases", ctypes.c_int), ("graph_steps", ctypes.c_int),
+                ("prefill_chunk", ctypes.c_int)]
 
 
 class Stats(ctypes.Structure):
@@ -58,12 +59,13 @@ def _ptr(a):
 
 class Engine:
     def __init__(self, path: str, max_context: int = 2048, eos: int = 2, loop_guard: bool = True,
-                 graph_steps: int = 16, verbose: bool = False, rope_theta: float = 0.0):
+                 graph_steps: int = 16, verbose: bool = False, rope_theta: float = 0.0, prefill_chunk: int = 0):
         o = Options()
         lib().cpi_engine_default_options(ctypes.byref(o))
         self._path = path.encode()
         o.model_path, o.max_context, o.eos_token_id = self._path, max_context, eos
         o.loop_guard, o.graph_steps, o.verbose, o.rope_theta = int(loop_guard), graph_steps, int(verbose), rope_theta
+        o.prefill_chunk = prefill_chunk
         self.h = lib().cpi_engine_create(ctypes.byref(o))
         if not self.h:
             raise RuntimeError(lib().cpi_engine_last_error().decode())

@@ -37,6 +37,10 @@ typedef struct cpi_engine_options {
   int verbose;              /* default 1 */
   int profile_decode_phases;/* default 0 */
   int graph_steps;          /* decode steps per graph launch; 0 = default (16) */
+  int prefill_chunk;        /* prompt tokens per chunked-prefill step (MFMA
+                               GEMMs); 0 = LLAMA_INFER_PREFILL_CHUNK_SIZE or
+                               128; 1 = token-by-token prefill
+                               (llama_engine.cpp:1077-1078) */
 } cpi_engine_options;
 
 /* engine::BenchmarkStats (llama_engine.hpp:102-127), scalar fields. */

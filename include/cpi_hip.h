@@ -186,12 +186,69 @@ int cpi_hip_attention_step_device_pos(const uint16_t* q,
 
 /* Causal prefill attention for a chunk whose K/V are already in the cache —
  * replaces launch_attention_prefill (kernels.cuh:316-325).  q/out fp16
- * [num_tokens, num_heads*head_dim]. */
+ * [num_tokens, num_heads*head_dim]; token t of the chunk is at cache
+ * position start_position + t and attends to positions [0, start+t]
+ * (exact softmax, fp32 statistics, fp16 P·V on MFMA).
+ * Preconditions: head_dim 64 or 128, num_heads % num_kv_heads == 0. */
 int cpi_hip_attention_prefill(const uint16_t* q, const uint16_t* k_cache,
                               const uint16_t* v_cache, uint16_t* out,
                               int num_tokens, int start_position,
                               int num_heads, int num_kv_heads, int head_dim,
                               cpi_stream_t stream);
+/* Same with a sliding window (> 0: keys (start+t-window, start+t]), the
+ * prefill counterpart of cpi_hip_attention_decode's sliding_window. */
+int cpi_hip_attention_prefill_window(const uint16_t* q, const uint16_t* k_cache,
+                                     const uint16_t* v_cache, uint16_t* out,
+                                     int num_tokens, int start_position,
+                                     int num_heads, int num_kv_heads,
+                                     int head_dim, int sliding_window,
+                                     cpi_stream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Chunked-prefill GEMM on MFMA: Y[m, n] = sum_k X[m, k] W[n, k] for a chunk
+ * of num_tokens rows, W in any CPI_W_* format (dequantised to fp16 in LDS,
+ * fp32 accumulation).  Replaces the cuBLASLt dispatch
+ * detail::dispatch_linear_rowmajor_weight (src/engine/llama_engine_internal.hpp:42-54,
+ * llama_engine.cpp:69-249) plus the rope/KV-copy/add/silu launches of
+ * prefill_prompt (llama_engine_generation.cpp:39-454).
+ *   x: fp16 [num_tokens, in_features] (16-byte aligned rows)
+ *   epilogue (rows ordered as for cpi_hip_gemv):
+ *     CPI_EPI_STORE_F32 / _F16   y [num_tokens, out_features]
+ *     CPI_EPI_RESID_ADD          y fp32 [num_tokens, out_features] +=
+ *     CPI_EPI_SWIGLU             y fp16 [num_tokens, out_features/2]
+ *     CPI_EPI_QKV_ROPE           y = q fp16 [num_tokens, num_heads*head_dim];
+ *                                k/v rows go to the cache at positions
+ *                                start_position + m
+ *   Preconditions: in_features % 64 == 0.
+ * ---------------------------------------------------------------------- */
+typedef struct cpi_gemm_desc {
+  int wfmt;
+  const void* w;
+  const void* scales;
+  int scale_count;
+  int out_features;
+  int in_features;
+  const uint16_t* x;
+  int num_tokens;
+  int epilogue;
+  void* y;
+  /* CPI_EPI_QKV_ROPE only */
+  int num_heads, num_kv_heads, head_dim;
+  int start_position;
+  const float* rope_cos;
+  const float* rope_sin;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int max_context;
+} cpi_gemm_desc;
+
+int cpi_hip_prefill_gemm(const cpi_gemm_desc* d, cpi_stream_t stream);
+
+/* Row RMSNorm of the fp32 residual stream into fp16 GEMM input:
+ * y[r, :] = fp16((x[r, :] * rsqrt(mean(x[r, :]^2) + eps)) * w) — the
+ * launch_norm of prefill_prompt (llama_engine.cpp:626-653) for fp32 rows. */
+int cpi_hip_rmsnorm_rows_f32(const float* x, const uint16_t* weight, uint16_t* y,
+                             int rows, int cols, float eps, cpi_stream_t stream);
 
 /* ------------------------------------------------------------------------
  * Small ops.

@@ -90,6 +90,36 @@ def test_engine_matches_oracle(tmp_path, name):
     eng.close()
 
 
+@pytest.mark.parametrize("name", ["f16_gqa_hd64", "i4g32_hd128", "f16_theta5e5_window", "i8_mha_hd64"])
+def test_chunked_prefill_matches_sequential(tmp_path, name):
+    """The MFMA chunked prefill (several chunks, a ragged last one) gives the
+    same next-token logits as token-by-token prefill and as the oracle."""
+    from cpi_amd.engine_py import Engine
+    cfg, attn, mlp, lm = CASES[name]
+    print(f"[prefill] case={name}", flush=True)
+    path = str(tmp_path / f"{name}.ll2c")
+    ll2c.write_synthetic(path, ll2c.SynthSpec(cfg, attn_fmt=attn, mlp_fmt=mlp, lm_fmt=lm, seed=7, std=0.02,
+                                              norm_jitter=0.1))
+    prompt = np.random.default_rng(2).integers(0, cfg.vocab_size, 101)
+    ref = oracle.Engine(path, 160)
+    for t, tok in enumerate(prompt[:-1]):
+        ref.forward(int(tok), t)
+    rl = ref.forward(int(prompt[-1]), len(prompt) - 1)
+    out = {}
+    for chunk in (1, 16, 0):
+        eng = Engine(path, max_context=160, eos=-1, loop_guard=False, prefill_chunk=chunk)
+        out[chunk] = eng.next_logits(prompt)
+        s = eng.stats()
+        eng.close()
+        err = np.abs(out[chunk] - rl).max()
+        print(f"[prefill] {name} chunk={chunk} max_abs_logit_err={err:.3e} prefill_ms={s['prefill_ms']:.2f}",
+              flush=True)
+        assert err <= LOGIT_TOL, (chunk, err)
+    assert np.abs(out[16] - out[1]).max() <= LOGIT_TOL
+    assert int(np.argmax(out[16])) == int(np.argmax(out[1])) or \
+        np.sort(rl)[-1] - np.sort(rl)[-2] <= 4 * LOGIT_TOL
+
+
 def test_engine_eos_and_empty_prompt(tmp_path):
     from cpi_amd.engine_py import Engine
     cfg = tiny_cfg()

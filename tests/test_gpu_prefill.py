@@ -1,0 +1,155 @@
+"""GPU parity of the chunked-prefill kernels (MFMA GEMM with fused epilogues,
+causal prefill attention) against the CPU oracle applied token by token, which
+is how the reference CPU engine consumes a prompt (cpu_engine.cpp:1064-1126).
+All calls go through the C-ABI (libcpi_hip.so)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from cpi_amd import _lib
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    from tests import gpu_util as G
+    from tests.test_gpu_kernels import FMTS, make_weights, _split_rows
+
+
+def gemm(fmt, w, s, sc_count, N, K, x16, M, y, epilogue=_lib.EPI_STORE_F32, **kw):
+    d = _lib.GemmDesc()
+    d.wfmt, d.w, d.scales, d.scale_count = FMTS[fmt], G.ptr(w), G.ptr(s), sc_count
+    d.out_features, d.in_features, d.x, d.num_tokens = N, K, G.ptr(x16), M
+    d.epilogue, d.y = epilogue, G.ptr(y)
+    for k, v in kw.items():
+        setattr(d, k, G.ptr(v) if isinstance(v, torch.Tensor) else v)
+    _lib.call("cpi_hip_prefill_gemm", ctypes.byref(d), G.stream())
+
+
+def row_bound(fmt, deq, x):
+    """|err| bound per (token, row): fp32 accumulation, plus the fp16 rounding
+    of q * group-scale for I4G32 (2^-11 relative per product)."""
+    c = 1.5e-3 if fmt == "i4g32" else 2e-5
+    return c * np.sqrt((x.astype(np.float64) ** 2) @ (deq.astype(np.float64) ** 2).T) + 1e-5
+
+
+@pytest.mark.parametrize("fmt", ["f16", "i8", "i4", "i4g32"])
+@pytest.mark.parametrize("N,K,M", [(64, 64, 1), (200, 192, 7), (384, 512, 64), (1000, 1024, 130),
+                                   (4096, 11008, 128)])
+def test_prefill_gemm_parity(fmt, N, K, M):
+    print(f"[pgemm] fmt={fmt} N={N} K={K} M={M}", flush=True)
+    blob, sc, deq = make_weights(fmt, N, K, N + K + M, random_lowbit=(N >= 4096))
+    x16 = np.random.default_rng(M).standard_normal((M, K)).astype(np.float16)
+    xf = x16.astype(np.float32)
+    y = G.empty(M * N * 4)
+    gemm(fmt, G.dev(blob), None if sc is None else G.dev(sc), 0 if sc is None else sc.size, N, K,
+         G.dev(x16), M, y)
+    got = G.host(y, np.float32, M * N).reshape(M, N)
+    rows = [0, M // 2, M - 1]
+    ref = np.stack([oracle.gemv(fmt, blob, sc, N, K, xf[m]) for m in rows])
+    bound = row_bound(fmt, deq, xf[rows])
+    err = np.abs(got[rows] - ref)
+    assert np.all(err <= bound), float((err / bound).max())
+    # every token against a float64 product of the dequantised weights
+    ref_all = xf.astype(np.float64) @ deq.astype(np.float64).T
+    assert np.all(np.abs(got - ref_all) <= row_bound(fmt, deq, xf) + 2e-5 * np.abs(ref_all))
+
+
+def test_prefill_gemm_global_scale_and_resid():
+    N, K, M = 128, 256, 5
+    rng = np.random.default_rng(3)
+    q = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    sc = np.array([0.0123], np.float32)
+    x16 = rng.standard_normal((M, K)).astype(np.float16)
+    base = rng.standard_normal((M, N)).astype(np.float32)
+    y = G.dev(base)
+    gemm("i8", G.dev(q), G.dev(sc), 1, N, K, G.dev(x16), M, y, epilogue=_lib.EPI_RESID_ADD)
+    ref = base + (x16.astype(np.float64) @ q.astype(np.float64).T) * 0.0123
+    np.testing.assert_allclose(G.host(y, np.float32, M * N).reshape(M, N), ref, rtol=1e-5, atol=1e-4)
+
+
+@pytest.mark.parametrize("fmt", ["f16", "i4g32"])
+def test_prefill_gemm_swiglu(fmt):
+    I, H, M = 320, 256, 33
+    blob, sc, deq = make_weights(fmt, 2 * I, H, 9)
+    order = np.zeros(2 * I, np.int32)
+    _lib.call("cpi_hip_swiglu_row_order", I, order.ctypes.data_as(ctypes.POINTER(ctypes.c_int)))
+    w, s = _split_rows(blob, sc, fmt, 2 * I, H)
+    x16 = np.random.default_rng(4).standard_normal((M, H)).astype(np.float16)
+    y = G.empty(M * I * 2)
+    gemm(fmt, G.dev(np.ascontiguousarray(w[order])), None if s is None else G.dev(np.ascontiguousarray(s[order])),
+         0 if s is None else s.size, 2 * I, H, G.dev(x16), M, y, epilogue=_lib.EPI_SWIGLU)
+    got = G.host(y, np.float16, M * I).reshape(M, I).astype(np.float32)
+    full = x16.astype(np.float64) @ deq.astype(np.float64).T
+    g, u = full[:, :I], full[:, I:]
+    ref = g / (1 + np.exp(-g)) * u
+    np.testing.assert_allclose(got, ref, atol=2e-3 * np.abs(ref).max() + 1e-4, rtol=2e-3)
+
+
+@pytest.mark.parametrize("fmt", ["f16", "i4g32", "i8"])
+@pytest.mark.parametrize("nh,nkv,hd", [(32, 4, 64), (8, 8, 128), (8, 2, 128)])
+def test_prefill_gemm_qkv_rope_kvstore(fmt, nh, nkv, hd):
+    H = 512 if fmt != "i8" else 256
+    R = (nh + 2 * nkv) * hd
+    max_ctx, start, M, theta = 96, 19, 40, 10000.0
+    rng = np.random.default_rng(nh + hd)
+    blob, sc, deq = make_weights(fmt, R, H, 21)
+    x16 = rng.standard_normal((M, H)).astype(np.float16)
+    order = np.zeros(R, np.int32)
+    _lib.call("cpi_hip_qkv_row_order", nh, nkv, hd, order.ctypes.data_as(ctypes.POINTER(ctypes.c_int)))
+    w, s = _split_rows(blob, sc, fmt, R, H)
+    cos_t, sin_t = oracle.rope_tables(max_ctx, hd, theta)
+    kc = G.empty(max_ctx * nkv * hd * 2)
+    vc = G.empty(max_ctx * nkv * hd * 2)
+    q = G.empty(M * nh * hd * 2)
+    gemm(fmt, G.dev(np.ascontiguousarray(w[order])), None if s is None else G.dev(np.ascontiguousarray(s[order])),
+         0 if s is None else s.size, R, H, G.dev(x16), M, q, epilogue=_lib.EPI_QKV_ROPE,
+         num_heads=nh, num_kv_heads=nkv, head_dim=hd, start_position=start, rope_cos=G.dev(cos_t),
+         rope_sin=G.dev(sin_t), k_cache=kc, v_cache=vc, max_context=max_ctx)
+    qh = G.host(q, np.float16, M * nh * hd).reshape(M, -1).astype(np.float32)
+    kch = G.host(kc, np.float16).reshape(max_ctx, -1).astype(np.float32)
+    vch = G.host(vc, np.float16).reshape(max_ctx, -1).astype(np.float32)
+    for m in range(M):
+        full = oracle.gemv(fmt, blob, sc, R, H, x16[m].astype(np.float32))
+        qr, kr = oracle.rope(full[:nh * hd], full[nh * hd:(nh + nkv) * hd], start + m, nh, nkv, hd, cos_t, sin_t)
+        vr = full[(nh + nkv) * hd:]
+        a = 4e-3 * np.abs(full).max() + 1e-4
+        np.testing.assert_allclose(qh[m], qr, atol=a)
+        np.testing.assert_allclose(kch[start + m], kr, atol=a)
+        np.testing.assert_allclose(vch[start + m], vr, atol=a)
+    untouched = np.r_[0:start, start + M:max_ctx]
+    assert not np.any(kch[untouched]) and not np.any(vch[untouched])
+
+
+@pytest.mark.parametrize("nh,nkv,hd,start,M,window", [
+    (8, 8, 128, 0, 1, 0), (8, 2, 128, 0, 70, 0), (32, 8, 128, 300, 128, 0), (32, 4, 64, 0, 128, 0),
+    (4, 4, 64, 37, 16, 0), (8, 2, 64, 100, 90, 45), (32, 32, 128, 384, 128, 0)])
+def test_attention_prefill_parity(nh, nkv, hd, start, M, window):
+    print(f"[attn_prefill] nh={nh} nkv={nkv} hd={hd} start={start} M={M} window={window}", flush=True)
+    rng = np.random.default_rng(start + M)
+    max_ctx = start + M + 5
+    kv = nkv * hd
+    kc = rng.standard_normal((max_ctx, kv)).astype(np.float16)
+    vc = rng.standard_normal((max_ctx, kv)).astype(np.float16)
+    q = rng.standard_normal((M, nh * hd)).astype(np.float16)
+    out = G.empty(M * nh * hd * 2)
+    _lib.call("cpi_hip_attention_prefill_window", G.ptr(G.dev(q)), G.ptr(G.dev(kc)), G.ptr(G.dev(vc)), G.ptr(out),
+              M, start, nh, nkv, hd, window, G.stream())
+    got = G.host(out, np.float16, M * nh * hd).reshape(M, -1).astype(np.float32)
+    kf, vf = kc.astype(np.float32), vc.astype(np.float32)
+    for t in sorted({0, M // 3, M // 2, M - 1}):
+        seq = start + t + 1
+        ref = oracle.attention(q[t].astype(np.float32), kf[:seq], vf[:seq], seq, nh, nkv, hd, window)
+        # P is rounded to fp16 before the P.V product (2^-11 relative), output fp16
+        np.testing.assert_allclose(got[t], ref, atol=4e-3, err_msg=f"token {t}")
+
+
+def test_prefill_rejects_bad_shapes():
+    d = _lib.GemmDesc()
+    x = G.empty(1024)
+    d.wfmt, d.w, d.x, d.y, d.out_features, d.in_features, d.num_tokens = 0, G.ptr(x), G.ptr(x), G.ptr(x), 8, 48, 1
+    assert _lib.lib().cpi_hip_prefill_gemm(ctypes.byref(d), G.stream()) == -1  # K % 64
+    assert _lib.lib().cpi_hip_attention_prefill(G.ptr(x), G.ptr(x), G.ptr(x), G.ptr(x), 1, 0, 4, 4, 96,
+                                                G.stream()) == -1  # head_dim
