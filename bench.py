@@ -138,6 +138,13 @@ def main():
             "kernel": "gemv_kernel<I4G32> w1|w3 22016x4096", "bytes_per_launch": dom["bytes"],
             "us_per_launch": dom["us"]}
 
+    # chunked-prefill GEMMs on MFMA (128-token chunk), kernel-only
+    pre = {}
+    for name, R, K in kbench.GEMV_SHAPES:
+        r = kbench.time_prefill_gemm("i4g32", R, K, 128)
+        pre[name] = {"us": round(r["us"], 2), "tflops": round(r["tflops"], 1), "mfma_frac": round(r["mfma_frac"], 4)}
+        log(f"[bench] prefill gemm {name} {R}x{K}x128: {r['us']:.1f} us, {r['tflops']:.0f} TFLOP/s")
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(path, args.cpu_seconds)
@@ -154,6 +161,7 @@ def main():
                    "parallelism": "single-gpu"},
         "prefill_tok_per_s": round(args.steps * (PROMPT_LEN - 1) / (prefill_ms / 1e3), 1),
         "gemv_i4g32": gemv,
+        "prefill_gemm_i4g32_m128": pre,
         "roofline": roof,
         "cpu_baseline": cpu,
     }

@@ -87,6 +87,11 @@ _SIGS = {
     "cpi_hip_scale_copy": (c_int, [c_void_p, c_void_p, c_int, c_float, c_void_p]),
     "cpi_hip_scale_add_inplace": (c_int, [c_void_p, c_void_p, c_int, c_float, c_void_p]),
     "cpi_hip_moe_router_topk_softmax": (c_int, [c_void_p, c_int, c_int, c_void_p, c_void_p, c_void_p]),
+    "cpi_hip_moe_router": (c_int, [c_void_p, c_void_p, c_float, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p,
+                                   c_void_p, c_void_p]),
+    "cpi_hip_moe_expert_gemv": (c_int, [ctypes.POINTER(GemvDesc), c_void_p, c_int, c_int, c_size_t, c_size_t,
+                                        c_size_t, c_size_t, c_void_p]),
+    "cpi_hip_moe_combine": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "cpi_hip_argmax_float": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
     "cpi_hip_greedy_advance": (c_int, [c_void_p] * 5 + [c_int, c_void_p]),
     "cpi_hip_prompt_advance": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p]),

@@ -112,7 +112,8 @@ int cpi_hip_weight_only_dual_matvec(int wfmt, const void* w_a, const void* sa, c
                      "weight_only_dual_matvec(b)");
 }
 
-int cpi_hip_gemv(const cpi_gemv_desc* d, cpi_stream_t s) {
+// Validates a GEMV descriptor and fills the kernel parameters (0 = ok).
+static int gemv_params(const cpi_gemv_desc* d, cpi::GemvParams& p) {
   if (!d) return fail("gemv: null descriptor");
   const int ce = cpi::gemv_elems_per_chunk(d->wfmt);
   if (ce == 0) return fail("gemv: unknown weight format");
@@ -128,7 +129,7 @@ int cpi_hip_gemv(const cpi_gemv_desc* d, cpi_stream_t s) {
     if (d->scale_count != 1 && d->scale_count != d->out_features)
       return fail("gemv: scale_count must be 1 or out_features");
   }
-  cpi::GemvParams p{};
+  p = cpi::GemvParams{};
   p.w = d->w;
   p.scales = d->scales;
   p.scale_count = d->scale_count;
@@ -159,7 +160,33 @@ int cpi_hip_gemv(const cpi_gemv_desc* d, cpi_stream_t s) {
   }
   if (d->epilogue < CPI_EPI_STORE_F32 || d->epilogue > CPI_EPI_QKV_ROPE)
     return fail("gemv: unknown epilogue");
+  return 0;
+}
+
+int cpi_hip_gemv(const cpi_gemv_desc* d, cpi_stream_t s) {
+  cpi::GemvParams p;
+  if (const int rc = gemv_params(d, p)) return rc;
   return check(cpi::gemv_launch(d->wfmt, d->epilogue, d->x_is_f32 != 0, p, S(s)), "gemv");
+}
+
+int cpi_hip_moe_expert_gemv(const cpi_gemv_desc* d, const int* expert_idx, int top_k, int num_experts,
+                            size_t expert_weight_bytes, size_t expert_scale_bytes, size_t x_slot_bytes,
+                            size_t y_slot_bytes, cpi_stream_t s) {
+  cpi::GemvParams p;
+  if (const int rc = gemv_params(d, p)) return rc;
+  if (!expert_idx || top_k <= 0 || top_k > 64 || num_experts <= 0)
+    return fail("moe_expert_gemv: need expert_idx, 1 <= top_k <= 64 and num_experts > 0");
+  if (d->epilogue == CPI_EPI_QKV_ROPE) return fail("moe_expert_gemv: QKV_ROPE is not a per-expert epilogue");
+  if (((expert_weight_bytes | expert_scale_bytes | x_slot_bytes) & 15) != 0)
+    return fail("moe_expert_gemv: expert and slot strides must keep 16-byte alignment");
+  p.expert_idx = expert_idx;
+  p.num_experts = num_experts;
+  p.num_slots = top_k;
+  p.w_estride = expert_weight_bytes;
+  p.s_estride = expert_scale_bytes;
+  p.x_sstride = x_slot_bytes;
+  p.y_sstride = y_slot_bytes;
+  return check(cpi::gemv_launch(d->wfmt, d->epilogue, d->x_is_f32 != 0, p, S(s)), "moe_expert_gemv");
 }
 
 int cpi_hip_qkv_row_order(int nh, int nkv, int hd, int* out) {
@@ -337,6 +364,24 @@ int cpi_hip_moe_router_topk_softmax(const uint16_t* logits, int experts, int top
   hipLaunchKernelGGL(cpi::router_topk_kernel, dim3(1), dim3(64), 0, S(s), logits, experts, top_k,
                      idx, prob);
   return check(hipGetLastError(), "moe_router_topk_softmax");
+}
+
+int cpi_hip_moe_router(const float* x, const uint16_t* norm_w, float eps, const uint16_t* router_w, int experts,
+                       int hidden, int top_k, int* idx, float* prob, float* logits_out, cpi_stream_t s) {
+  if (!x || !norm_w || !router_w || !idx || !prob) return fail("moe_router: null pointer");
+  if (experts <= 0 || experts > 64 || top_k <= 0 || top_k > experts)
+    return fail("moe_router: experts must be in [1, 64] and 1 <= top_k <= experts");
+  if (hidden <= 0 || hidden > 256 * cpi::kRouterMaxPer) return fail("moe_router: hidden must be in [1, 8192]");
+  hipLaunchKernelGGL(cpi::moe_router_kernel, dim3(1), dim3(256), 0, S(s), x, norm_w, eps, router_w, experts, hidden,
+                     top_k, idx, prob, logits_out);
+  return check(hipGetLastError(), "moe_router");
+}
+
+int cpi_hip_moe_combine(float* x, const float* y, const float* prob, int top_k, int hidden, cpi_stream_t s) {
+  if (!x || !y || !prob || top_k <= 0 || hidden <= 0) return fail("moe_combine: bad arguments");
+  hipLaunchKernelGGL(cpi::moe_combine_kernel, dim3((hidden + 255) / 256), dim3(256), 0, S(s), x, y, prob, top_k,
+                     hidden);
+  return check(hipGetLastError(), "moe_combine");
 }
 
 int cpi_hip_argmax_float(const float* x, int n, int* out, cpi_stream_t s) {

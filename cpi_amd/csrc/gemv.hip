@@ -74,6 +74,13 @@ struct GemvParams {
   uint16_t* k_cache;
   uint16_t* v_cache;
   int max_ctx;
+  // Gathered experts (MoE): when expert_idx != nullptr, grid.y = top-k slots;
+  // slot j uses expert e = expert_idx[j] whose weights / scales start
+  // e * w_estride / e * s_estride bytes past w / scales, reads x at
+  // j * x_sstride bytes and writes y at j * y_sstride bytes.
+  const int* expert_idx;
+  int num_experts, num_slots;
+  size_t w_estride, s_estride, x_sstride, y_sstride;
 };
 
 enum { EPI_DUAL_F16 = 100 };
@@ -427,6 +434,14 @@ __device__ __forceinline__ void row_epilogue(const GemvParams& p, int epi, int r
 // ---------------------------------------------------------------------------
 template <int FMT, bool XF32, int NR, int PP, int MAXU>
 __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int epi, int ks) {
+  if (p.expert_idx != nullptr) {
+    int e = __builtin_amdgcn_readfirstlane(p.expert_idx[blockIdx.y]);
+    e = e < 0 ? 0 : (e >= p.num_experts ? p.num_experts - 1 : e);
+    p.w = static_cast<const uint8_t*>(p.w) + static_cast<size_t>(e) * p.w_estride;
+    if (p.scales != nullptr) p.scales = static_cast<const uint8_t*>(p.scales) + static_cast<size_t>(e) * p.s_estride;
+    p.x = static_cast<const uint8_t*>(p.x) + static_cast<size_t>(blockIdx.y) * p.x_sstride;
+    p.y = static_cast<uint8_t*>(p.y) + static_cast<size_t>(blockIdx.y) * p.y_sstride;
+  }
   using F = FmtT<FMT>;
   extern __shared__ __align__(16) uint32_t lds[];
   __shared__ float red[kWavesPerBlock];
@@ -658,7 +673,8 @@ hipError_t launch_kernel(const GemvParams& p, int epi, const GemvPlan& g, size_t
     if (e != hipSuccess) return e;
     lds_set = lds;
   }
-  hipLaunchKernelGGL((gemv_kernel<FMT, XF32, NR, PP, MAXU>), dim3(g.grid), dim3(kBlock), lds, s, p, epi, g.ks);
+  const int slots = p.expert_idx != nullptr ? p.num_slots : 1;
+  hipLaunchKernelGGL((gemv_kernel<FMT, XF32, NR, PP, MAXU>), dim3(g.grid, slots), dim3(kBlock), lds, s, p, epi, g.ks);
   return hipGetLastError();
 }
 

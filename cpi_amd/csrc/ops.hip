@@ -96,15 +96,13 @@ __global__ void scale_add_kernel(uint16_t* dst, const uint16_t* src, int n, floa
 // ---- MoE router: softmax over experts, greedy top-k with strict '>',
 //      renormalised over the picked experts (kernels_ops_matvec.cu:115-193,
 //      cpu_engine.cpp:560-606).  Single thread: experts <= 64.
-__global__ void router_topk_kernel(const uint16_t* logits, int experts, int top_k, int* idx,
-                                   float* prob) {
-  if (threadIdx.x != 0) return;
+__device__ void topk_softmax(const float* lg, int experts, int top_k, int* idx, float* prob) {
   float pr[64];
-  float mx = h2f(logits[0]);
-  for (int e = 1; e < experts; ++e) mx = fmaxf(mx, h2f(logits[e]));
+  float mx = lg[0];
+  for (int e = 1; e < experts; ++e) mx = fmaxf(mx, lg[e]);
   float sum = 0.f;
   for (int e = 0; e < experts; ++e) {
-    pr[e] = expf(h2f(logits[e]) - mx);
+    pr[e] = expf(lg[e] - mx);
     sum += pr[e];
   }
   const float inv = 1.f / fmaxf(sum, 1e-8f);
@@ -131,6 +129,69 @@ __global__ void router_topk_kernel(const uint16_t* logits, int experts, int top_
     idx[k] = k < kk ? pick[k] : 0;
     prob[k] = k < kk ? pp[k] * ip : 0.f;
   }
+}
+
+__global__ void router_topk_kernel(const uint16_t* logits, int experts, int top_k, int* idx,
+                                   float* prob) {
+  if (threadIdx.x != 0) return;
+  float lg[64];
+  for (int e = 0; e < experts; ++e) lg[e] = h2f(logits[e]);
+  topk_softmax(lg, experts, top_k, idx, prob);
+}
+
+// ---- Fused decode router: RMSNorm of the fp32 residual (fp32 statistics,
+//      cpu_engine.cpp:392-405 order), router logits against fp16 router rows
+//      [experts, hidden] in fp32, then the top-k softmax above — the router
+//      matvec + moe_router_topk_softmax of llama_engine_forward_decode.cpp:
+//      395-426 as one launch with no host round trip.  One block of 256.
+constexpr int kRouterMaxPer = 32;  // hidden <= 256 * 32
+__global__ void __launch_bounds__(256) moe_router_kernel(const float* x, const uint16_t* norm_w, float eps,
+                                                         const uint16_t* rw, int experts, int hidden, int top_k,
+                                                         int* idx, float* prob, float* logits_out) {
+  __shared__ float red[4];
+  __shared__ float lg[64];
+  float xn[kRouterMaxPer];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kRouterMaxPer; ++j) {
+    const int i = threadIdx.x + 256 * j;
+    xn[j] = i < hidden ? x[i] : 0.f;
+    ss += xn[j] * xn[j];
+  }
+  ss = block_sum(ss, red);
+  const float inv = 1.f / sqrtf(ss / static_cast<float>(hidden) + eps);
+#pragma unroll
+  for (int j = 0; j < kRouterMaxPer; ++j) {
+    const int i = threadIdx.x + 256 * j;
+    xn[j] = i < hidden ? inv * xn[j] * h2f(norm_w[i]) : 0.f;
+  }
+  for (int e = 0; e < experts; ++e) {
+    const uint16_t* r = rw + static_cast<size_t>(e) * hidden;
+    float d = 0.f;
+#pragma unroll
+    for (int j = 0; j < kRouterMaxPer; ++j) {
+      const int i = threadIdx.x + 256 * j;
+      if (i < hidden) d += xn[j] * h2f(r[i]);
+    }
+    d = block_sum(d, red);
+    if (threadIdx.x == 0) lg[e] = d;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (logits_out)
+      for (int e = 0; e < experts; ++e) logits_out[e] = lg[e];
+    topk_softmax(lg, experts, top_k, idx, prob);
+  }
+}
+
+// ---- MoE combine: x[i] += sum_k prob[k] * y[k][i], accumulated in slot order
+//      into a zeroed sum first (cpu_engine.cpp:600-606 order).
+__global__ void moe_combine_kernel(float* x, const float* y, const float* prob, int top_k, int hidden) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= hidden) return;
+  float acc = 0.f;
+  for (int k = 0; k < top_k; ++k) acc += prob[k] * y[static_cast<size_t>(k) * hidden + i];
+  x[i] += acc;
 }
 
 // ---- argmax with the CPU engine's tie rule (std::max_element: lowest index

@@ -134,8 +134,20 @@ LlamaEngine::HostLinear LlamaEngine::bind_linear(const std::string& name, int ro
 
 // Concatenates the row blocks of `parts` (same format, same K) and stores them
 // on the device in the row order `order` (device row i = logical row order[i]).
+std::size_t LlamaEngine::weight_bytes_of(const Linear& L) {
+  const std::size_t K = static_cast<std::size_t>(L.cols);
+  const std::size_t rb = L.wfmt == CPI_W_F16 ? 2 * K : (L.wfmt == CPI_W_I8ROW ? K : (K + 1) / 2);
+  return rb * static_cast<std::size_t>(L.rows);
+}
+
+std::size_t LlamaEngine::scale_bytes_of(const Linear& L) {
+  if (L.wfmt == CPI_W_I4G32) return static_cast<std::size_t>(L.rows) * ((L.cols + 31) / 32) * 2;
+  if (L.wfmt == CPI_W_F16) return 0;
+  return static_cast<std::size_t>(L.rows) * 4;
+}
+
 LlamaEngine::Linear LlamaEngine::upload_fused(const std::vector<HostLinear>& parts,
-                                              const std::vector<int>& order) {
+                                              const std::vector<int>& order, void* dst_w, void* dst_s) {
   Linear L;
   L.wfmt = parts[0].wfmt;
   L.cols = parts[0].cols;
@@ -155,8 +167,8 @@ LlamaEngine::Linear LlamaEngine::upload_fused(const std::vector<HostLinear>& par
     HIP_OK(hipMemcpy(d_order, order.data(), order.size() * sizeof(int), hipMemcpyHostToDevice));
   }
   auto place = [&](const std::vector<std::pair<const std::byte*, std::size_t>>& blocks,
-                   std::size_t rb) -> void* {
-    void* dst = dmalloc(rb * L.rows);
+                   std::size_t rb, void* given) -> void* {
+    void* dst = given ? given : dmalloc(rb * L.rows);
     void* stage = dst;
     if (!identity) HIP_OK(hipMalloc(&stage, rb * L.rows));
     std::size_t off = 0;
@@ -174,13 +186,13 @@ LlamaEngine::Linear LlamaEngine::upload_fused(const std::vector<HostLinear>& par
   };
   std::vector<std::pair<const std::byte*, std::size_t>> wblocks;
   for (const auto& p : parts) wblocks.push_back({p.w, p.w_bytes});
-  L.w = place(wblocks, row_bytes);
+  L.w = place(wblocks, row_bytes, dst_w);
   (void)total;
 
   if (L.wfmt == CPI_W_I4G32) {
     std::vector<std::pair<const std::byte*, std::size_t>> sblocks;
     for (const auto& p : parts) sblocks.push_back({p.scales, p.scale_bytes});
-    L.scales = place(sblocks, ((K + 31) / 32) * 2);
+    L.scales = place(sblocks, ((K + 31) / 32) * 2, dst_s);
     L.scale_count = L.rows * static_cast<int>((K + 31) / 32);
   } else if (L.wfmt != CPI_W_F16) {
     // per-row fp32 scales (a single global scale is expanded per row)
@@ -194,7 +206,7 @@ LlamaEngine::Linear LlamaEngine::upload_fused(const std::vector<HostLinear>& par
         s.push_back(v);
       }
     }
-    L.scales = place({{reinterpret_cast<const std::byte*>(s.data()), s.size() * 4}}, 4);
+    L.scales = place({{reinterpret_cast<const std::byte*>(s.data()), s.size() * 4}}, 4, dst_s);
     L.scale_count = L.rows;
   }
   if (d_order) HIP_OK(hipFree(d_order));
@@ -212,7 +224,6 @@ void LlamaEngine::initialize(const EngineOptions& options) {
   file_.open(opts_.model_path);
   cfg_ = file_.config();
   if (cfg_.use_layernorm || cfg_.has_qkv_bias) ENGINE_THROW("LayerNorm / QKV-bias models are not supported");
-  if (cfg_.is_moe()) ENGINE_THROW("MoE models are not supported by this engine yet");
   const int H = cfg_.hidden_size, I = cfg_.intermediate_size, V = cfg_.vocab_size;
   const int NL = cfg_.num_layers, NH = cfg_.num_heads, NKV = cfg_.num_kv_heads;
 
@@ -253,6 +264,16 @@ void LlamaEngine::initialize(const EngineOptions& options) {
   CPI_OK(cpi_hip_qkv_row_order(NH, NKV, head_dim_, qkv_order.data()));
   std::vector<int> glu_order(static_cast<std::size_t>(2 * I));
   CPI_OK(cpi_hip_swiglu_row_order(I, glu_order.data()));
+  std::vector<int> moe_glu_order;
+  if (cfg_.is_moe()) {
+    moe_experts_ = cfg_.num_local_experts;
+    moe_inter_ = cfg_.effective_expert_intermediate_size();
+    moe_top_k_ = cfg_.num_experts_per_tok > 0 ? cfg_.num_experts_per_tok : 2;  // cpu_engine.cpp:563-566
+    moe_top_k_ = std::min(moe_top_k_, moe_experts_);
+    if (moe_experts_ > 64) ENGINE_THROW("at most 64 experts are supported");
+    moe_glu_order.resize(static_cast<std::size_t>(2 * moe_inter_));
+    CPI_OK(cpi_hip_swiglu_row_order(moe_inter_, moe_glu_order.data()));
+  }
   const std::size_t kv_bytes = static_cast<std::size_t>(opts_.max_context) * kv_dim_ * 2;
   layers_.resize(static_cast<std::size_t>(NL));
   for (int l = 0; l < NL; ++l) {
@@ -265,9 +286,48 @@ void LlamaEngine::initialize(const EngineOptions& options) {
                           bind_linear(p + "attention.wv", kv_dim_, H)},
                          qkv_order);
     L.wo = upload_fused({bind_linear(p + "attention.wo", H, q_dim_)}, {});
-    L.w13 = upload_fused({bind_linear(p + "feed_forward.w1", I, H), bind_linear(p + "feed_forward.w3", I, H)},
-                         glu_order);
-    L.w2 = upload_fused({bind_linear(p + "feed_forward.w2", H, I)}, {});
+    if (cfg_.is_moe()) {
+      // router + all experts resident (replaces the per-token H2D expert
+      // streaming of llama_engine_forward_decode.cpp:139-276)
+      L.moe = true;
+      const int E = moe_experts_, EI = moe_inter_;
+      const HostLinear r = bind_linear(p + "feed_forward.router", E, H);
+      if (r.wfmt != CPI_W_F16) ENGINE_THROW("MoE router weights must be fp16");
+      L.router = upload_fused({r}, {});
+      for (int e = 0; e < E; ++e) {
+        const std::string b = p + "feed_forward.experts." + std::to_string(e) + ".";
+        const std::vector<HostLinear> w13p = {bind_linear(b + "w1", EI, H), bind_linear(b + "w3", EI, H)};
+        const std::vector<HostLinear> w2p = {bind_linear(b + "w2", H, EI)};
+        if (e == 0) {
+          // expert 0 allocates room for all E experts
+          Linear probe13, probe2;
+          probe13.wfmt = w13p[0].wfmt; probe13.rows = 2 * EI; probe13.cols = H;
+          probe2.wfmt = w2p[0].wfmt; probe2.rows = H; probe2.cols = EI;
+          L.ew13_w_stride = weight_bytes_of(probe13);
+          L.ew13_s_stride = scale_bytes_of(probe13);
+          L.ew2_w_stride = weight_bytes_of(probe2);
+          L.ew2_s_stride = scale_bytes_of(probe2);
+          void* w13 = dmalloc(L.ew13_w_stride * E);
+          void* s13 = L.ew13_s_stride ? dmalloc(L.ew13_s_stride * E) : nullptr;
+          void* w2 = dmalloc(L.ew2_w_stride * E);
+          void* s2 = L.ew2_s_stride ? dmalloc(L.ew2_s_stride * E) : nullptr;
+          L.ew13 = upload_fused(w13p, moe_glu_order, w13, s13);
+          L.ew2 = upload_fused(w2p, {}, w2, s2);
+        } else {
+          auto off = [](void* base, std::size_t stride, int i) -> void* {
+            return base ? static_cast<char*>(base) + stride * static_cast<std::size_t>(i) : nullptr;
+          };
+          const Linear a = upload_fused(w13p, moe_glu_order, off(L.ew13.w, L.ew13_w_stride, e),
+                                        off(L.ew13.scales, L.ew13_s_stride, e));
+          const Linear c = upload_fused(w2p, {}, off(L.ew2.w, L.ew2_w_stride, e), off(L.ew2.scales, L.ew2_s_stride, e));
+          if (a.wfmt != L.ew13.wfmt || c.wfmt != L.ew2.wfmt) ENGINE_THROW("all experts of a layer need one format");
+        }
+      }
+    } else {
+      L.w13 = upload_fused({bind_linear(p + "feed_forward.w1", I, H), bind_linear(p + "feed_forward.w3", I, H)},
+                           glu_order);
+      L.w2 = upload_fused({bind_linear(p + "feed_forward.w2", H, I)}, {});
+    }
     L.k_cache = static_cast<uint16_t*>(dmalloc(kv_bytes));
     L.v_cache = static_cast<uint16_t*>(dmalloc(kv_bytes));
   }
@@ -286,6 +346,12 @@ void LlamaEngine::initialize(const EngineOptions& options) {
   q_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(q_dim_) * 4));
   att_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(q_dim_) * 4));
   ff_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(I) * 4));
+  if (cfg_.is_moe()) {
+    d_moe_idx_ = static_cast<int*>(dmalloc(static_cast<std::size_t>(moe_top_k_) * 4));
+    d_moe_prob_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(moe_top_k_) * 4));
+    moe_ff_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(moe_top_k_) * moe_inter_ * 4));
+    moe_y_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(moe_top_k_) * H * 4));
+  }
   logits_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(V) * 4));
   attn_scratch_ = static_cast<float*>(dmalloc(cpi_hip_attention_scratch_floats(NH, head_dim_) * 4));
   HIP_OK(hipMemset(attn_scratch_, 0, cpi_hip_attention_scratch_floats(NH, head_dim_) * 4));
@@ -309,7 +375,9 @@ void LlamaEngine::initialize(const EngineOptions& options) {
       if (const char* env = std::getenv("LLAMA_INFER_PREFILL_CHUNK_SIZE")) chunk = std::max(1, std::atoi(env));
     }
     chunk = std::min(chunk, opts_.max_context);
-    const bool shapes_ok = H % 64 == 0 && q_dim_ % 64 == 0 && I % 64 == 0 && (head_dim_ == 64 || head_dim_ == 128);
+    // MoE prompts run token by token, as in the reference
+    // (llama_engine_generation.cpp:45-48)
+    const bool shapes_ok = !cfg_.is_moe() && H % 64 == 0 && q_dim_ % 64 == 0 && I % 64 == 0 && (head_dim_ == 64 || head_dim_ == 128);
     prefill_chunk_ = shapes_ok ? chunk : 1;
     if (prefill_chunk_ > 1) {
       const std::size_t C = static_cast<std::size_t>(prefill_chunk_);
@@ -359,6 +427,27 @@ void LlamaEngine::enqueue_step(bool with_head) {
     o.epilogue = CPI_EPI_RESID_ADD; o.y = x_;
     CPI_OK(cpi_hip_gemv(&o, stream_));
 
+    if (L.moe) {
+      // router + top-k on device, both selected experts in one launch each,
+      // then x += sum_k p_k y_k
+      CPI_OK(cpi_hip_moe_router(x_, L.norm_ffn, cfg_.norm_eps, static_cast<const uint16_t*>(L.router.w),
+                                moe_experts_, H, moe_top_k_, d_moe_idx_, d_moe_prob_, nullptr, stream_));
+      const int EI = moe_inter_;
+      cpi_gemv_desc g{};
+      g.wfmt = L.ew13.wfmt; g.w = L.ew13.w; g.scales = L.ew13.scales; g.scale_count = L.ew13.scale_count;
+      g.out_features = 2 * EI; g.in_features = H; g.x = x_; g.x_is_f32 = 1;
+      g.norm_w = L.norm_ffn; g.norm_eps = cfg_.norm_eps; g.epilogue = CPI_EPI_SWIGLU; g.y = moe_ff_;
+      CPI_OK(cpi_hip_moe_expert_gemv(&g, d_moe_idx_, moe_top_k_, moe_experts_, L.ew13_w_stride, L.ew13_s_stride, 0,
+                                     static_cast<std::size_t>(EI) * 4, stream_));
+      cpi_gemv_desc w{};
+      w.wfmt = L.ew2.wfmt; w.w = L.ew2.w; w.scales = L.ew2.scales; w.scale_count = L.ew2.scale_count;
+      w.out_features = H; w.in_features = EI; w.x = moe_ff_; w.x_is_f32 = 1;
+      w.epilogue = CPI_EPI_STORE_F32; w.y = moe_y_;
+      CPI_OK(cpi_hip_moe_expert_gemv(&w, d_moe_idx_, moe_top_k_, moe_experts_, L.ew2_w_stride, L.ew2_s_stride,
+                                     static_cast<std::size_t>(EI) * 4, static_cast<std::size_t>(H) * 4, stream_));
+      CPI_OK(cpi_hip_moe_combine(x_, moe_y_, d_moe_prob_, moe_top_k_, H, stream_));
+      continue;
+    }
     cpi_gemv_desc g{};
     g.wfmt = L.w13.wfmt; g.w = L.w13.w; g.scales = L.w13.scales; g.scale_count = L.w13.scale_count;
     g.out_features = 2 * I; g.in_features = H; g.x = x_; g.x_is_f32 = 1;

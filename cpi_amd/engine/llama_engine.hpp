@@ -125,6 +125,11 @@ class LlamaEngine {
   };
   struct Layer {
     Linear qkv, wo, w13, w2;
+    // MoE: router (fp16 [E, H]) and all experts back to back; ew13 / ew2
+    // describe expert 0, later experts follow at the *_stride byte offsets
+    bool moe = false;
+    Linear router, ew13, ew2;
+    std::size_t ew13_w_stride = 0, ew13_s_stride = 0, ew2_w_stride = 0, ew2_s_stride = 0;
     uint16_t* norm_att = nullptr;
     uint16_t* norm_ffn = nullptr;
     uint16_t* k_cache = nullptr;
@@ -141,7 +146,12 @@ class LlamaEngine {
     int rows = 0, cols = 0;
   };
   HostLinear bind_linear(const std::string& name, int rows, int cols) const;
-  Linear upload_fused(const std::vector<HostLinear>& parts, const std::vector<int>& order);
+  // Uploads the row blocks of `parts`; with dst_w (and dst_s for scaled
+  // formats) given, writes into that device memory instead of allocating.
+  Linear upload_fused(const std::vector<HostLinear>& parts, const std::vector<int>& order,
+                      void* dst_w = nullptr, void* dst_s = nullptr);
+  static std::size_t weight_bytes_of(const Linear& L);
+  static std::size_t scale_bytes_of(const Linear& L);
   void* dmalloc(std::size_t bytes);
   uint16_t* upload_f16(const std::string& name, std::size_t expect_bytes);
 
@@ -169,6 +179,10 @@ class LlamaEngine {
 
   float *x_ = nullptr, *q_ = nullptr, *att_ = nullptr, *ff_ = nullptr, *logits_ = nullptr;
   float* attn_scratch_ = nullptr;
+  // MoE decode state: selected experts / weights per token, expert outputs
+  int moe_experts_ = 0, moe_top_k_ = 0, moe_inter_ = 0;
+  int* d_moe_idx_ = nullptr;
+  float *d_moe_prob_ = nullptr, *moe_ff_ = nullptr, *moe_y_ = nullptr;
   int *d_token_ = nullptr, *d_pos_ = nullptr, *d_step_ = nullptr, *d_ring_ = nullptr,
       *d_prompt_ = nullptr;
   int ring_len_ = 16;

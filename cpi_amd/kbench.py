@@ -95,6 +95,54 @@ def time_gemv(fmt: str, R: int, K: int, rotate_bytes: int = 3 << 30, iters: int 
     return {"fmt": fmt, "R": R, "K": K, "us": us, "bytes": nbytes, "gbps": nbytes / us / 1e3}
 
 
+PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+
+
+def time_prefill_gemm(fmt: str, N: int, K: int, M: int = 128, iters: int = 50, rotate_bytes: int = 1 << 30):
+    """Kernel-only chunked-prefill GEMM: M tokens x (N x K) weights, plain fp32
+    store.  Returns dict(us, tflops, mfma_frac)."""
+    gen = torch.Generator(device="cuda").manual_seed(N + K + M)
+    wbytes = gemv_bytes(fmt, N, K)
+    copies = max(2, int(np.ceil(rotate_bytes / wbytes)))
+    bufs = [_weights(fmt, N, K, gen) for _ in range(copies)]
+    x = torch.randn(M * K, device="cuda", generator=gen).half()
+    y = torch.empty(M * N, device="cuda", dtype=torch.float32)
+    descs = []
+    for w, s, sc in bufs:
+        d = _lib.GemmDesc()
+        d.wfmt, d.w, d.scales, d.scale_count = FMT_CODE[fmt], w.data_ptr(), (s.data_ptr() if s is not None else 0), sc
+        d.out_features, d.in_features, d.x, d.num_tokens = N, K, x.data_ptr(), M
+        d.epilogue, d.y = _lib.EPI_STORE_F32, y.data_ptr()
+        descs.append(d)
+    fn = _lib.lib().cpi_hip_prefill_gemm
+
+    def launch_all(n):
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        for i in range(n):
+            rc = fn(ctypes.byref(descs[i % copies]), st)
+            if rc:
+                raise _lib.CpiHipError(_lib.lib().cpi_hip_last_error_string().decode())
+
+    launch_all(copies)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        launch_all(iters)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / iters
+    tflops = 2.0 * M * N * K / us / 1e6
+    del g, bufs
+    torch.cuda.empty_cache()
+    return {"fmt": fmt, "N": N, "K": K, "M": M, "us": us, "tflops": tflops, "mfma_frac": tflops / PEAK_F16_TFLOPS,
+            "weight_gbps": wbytes / us / 1e3}
+
+
 def time_attention(nh, nkv, hd, ctx, iters=100, rotate_bytes=2 << 30):
     gen = torch.Generator(device="cuda").manual_seed(ctx)
     kvb = ctx * nkv * hd * 2 * 2
@@ -171,6 +219,13 @@ if __name__ == "__main__":
     import sys
     if sys.argv[1:2] == ["pmc"]:
         pmc_workload()
+        sys.exit(0)
+    if sys.argv[1:2] == ["prefill"]:
+        for f in ("i4g32", "f16"):
+            for name, R, K in GEMV_SHAPES:
+                r = time_prefill_gemm(f, R, K)
+                r["shape"] = name
+                print(json.dumps(r), flush=True)
         sys.exit(0)
     fmts = sys.argv[1:] or ["i4g32", "i4", "i8", "f16"]
     for f in fmts:

@@ -302,6 +302,36 @@ int cpi_hip_scale_add_inplace(uint16_t* dst, const uint16_t* src, int n,
 int cpi_hip_moe_router_topk_softmax(const uint16_t* logits, int experts,
                                     int top_k, int* topk_idx, float* topk_prob,
                                     cpi_stream_t stream);
+/* ------------------------------------------------------------------------
+ * Resident MoE decode (batch 1, no host round trip).  Replaces the router
+ * matvec + launch_moe_router_topk_softmax, the per-expert H2D weight copies
+ * and matvecs, and the host-synchronised merge of
+ * src/engine/llama_engine_forward_decode.cpp:97-498.
+ * ---------------------------------------------------------------------- */
+/* Router: xn = rmsnorm(x) * norm_w (fp32), logits[e] = xn . router_w[e]
+ * (fp16 [experts, hidden], fp32 accumulate), softmax over experts, greedy
+ * top-k with strict '>' and renormalisation (kernels_ops_matvec.cu:115-193).
+ * topk_idx int [top_k], topk_prob fp32 [top_k]; logits_out fp32 [experts] or
+ * NULL.  experts <= 64, hidden <= 8192. */
+int cpi_hip_moe_router(const float* x, const uint16_t* norm_w, float eps,
+                       const uint16_t* router_w, int experts, int hidden,
+                       int top_k, int* topk_idx, float* topk_prob,
+                       float* logits_out, cpi_stream_t stream);
+/* Gathered expert GEMV: one launch runs top_k slots; slot j uses expert
+ * e = expert_idx[j] (device), whose weights / scales begin
+ * e * expert_weight_bytes / e * expert_scale_bytes past d->w / d->scales
+ * (all experts of a layer stored back to back), reads x at
+ * j * x_slot_bytes past d->x and writes its epilogue output at
+ * j * y_slot_bytes past d->y.  Any epilogue except CPI_EPI_QKV_ROPE. */
+int cpi_hip_moe_expert_gemv(const cpi_gemv_desc* d, const int* expert_idx,
+                            int top_k, int num_experts,
+                            size_t expert_weight_bytes,
+                            size_t expert_scale_bytes, size_t x_slot_bytes,
+                            size_t y_slot_bytes, cpi_stream_t stream);
+/* x[i] += sum_k topk_prob[k] * y[k * hidden + i]  (slot order, fp32). */
+int cpi_hip_moe_combine(float* x, const float* y, const float* topk_prob,
+                        int top_k, int hidden, cpi_stream_t stream);
+
 /* launch_argmax_float (kernels.cuh:785-788): lowest index among maxima. */
 int cpi_hip_argmax_float(const float* logits, int n, int* out_index,
                          cpi_stream_t stream);

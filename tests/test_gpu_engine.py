@@ -28,6 +28,8 @@ CASES = {
     "i4row_mlp": (tiny_cfg(), "f16", "i4", "f16"),
     "i4g32_hd128": (tiny_cfg(hidden_size=512, num_heads=4, num_kv_heads=1, intermediate_size=1024), "i4g32",
                     "i4g32", "f16"),
+    "moe_top2_i4g32": (tiny_cfg(num_local_experts=4, num_experts_per_tok=2, expert_intermediate_size=384,
+                                num_kv_heads=1), "i4g32", "i4g32", "f16"),
     "f16_theta5e5_window": (tiny_cfg(rope_theta=500000.0, sliding_window=40, num_heads=8, num_kv_heads=1,
                                      hidden_size=512), "f16", "f16", "f16"),
 }

@@ -303,3 +303,82 @@ def test_small_ops():
     assert (G.host(un, np.int8, 256) == qv).all() and np.abs(qv).max() <= 7
     scv = G.host(sc, np.float32, 4)
     np.testing.assert_allclose(scv, np.abs(m.astype(np.float32)).max(1) / 7, rtol=1e-6)
+
+
+def test_moe_router_matches_oracle():
+    """Fused RMSNorm + router logits + top-k softmax against the oracle
+    (cpu_engine.cpp:561-606); includes the reference's own KAT logits."""
+    rng = np.random.default_rng(11)
+    H, E, K = 4096, 8, 2
+    x = rng.standard_normal(H).astype(np.float32) * 3
+    nw = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
+    rw = (rng.standard_normal((E, H)) * 0.02).astype(np.float16)
+    idx, prob, lg = G.empty(16), G.empty(16), G.empty(64)
+    _lib.call("cpi_hip_moe_router", G.ptr(G.dev(x)), G.ptr(G.dev(nw)), 1e-5, G.ptr(G.dev(rw)), E, H, K,
+              G.ptr(idx), G.ptr(prob), G.ptr(lg), G.stream())
+    xn = oracle.rmsnorm(x, nw, 1e-5)
+    ref_lg = oracle.gemv("f16", rw.view(np.uint8).reshape(-1), None, E, H, xn)
+    np.testing.assert_allclose(G.host(lg, np.float32, E), ref_lg, rtol=1e-4, atol=1e-4)
+    ri, rp = oracle.router_topk(ref_lg, K)
+    assert list(G.host(idx, np.int32, K)) == list(ri)
+    np.testing.assert_allclose(G.host(prob, np.float32, K), rp, rtol=1e-5)
+
+
+@pytest.mark.parametrize("fmt", ["i4g32", "i8", "f16"])
+def test_moe_expert_gemv_and_combine(fmt):
+    """Gathered expert GEMVs (both selected experts in one launch) equal the
+    plain GEMV of each selected expert; combine adds sum_k p_k y_k."""
+    E, EI, H, K = 4, 256, 512, 2
+    rng = np.random.default_rng(12)
+    order = np.zeros(2 * EI, np.int32)
+    _lib.call("cpi_hip_swiglu_row_order", EI, order.ctypes.data_as(ctypes.POINTER(ctypes.c_int)))
+    w13, s13, w2, s2 = [], [], [], []
+    for e in range(E):
+        b, s, _ = make_weights(fmt, 2 * EI, H, 100 + e)
+        wr, sr = _split_rows(b, s, fmt, 2 * EI, H)
+        w13.append(np.ascontiguousarray(wr[order]))
+        s13.append(None if sr is None else np.ascontiguousarray(sr[order]))
+        b2, s2_, _ = make_weights(fmt, H, EI, 200 + e)
+        w2.append(b2)
+        s2.append(s2_)
+    cat = lambda parts: np.concatenate([p.reshape(-1) for p in parts])
+    W13, W2 = G.dev(cat(w13)), G.dev(cat(w2))
+    S13 = None if s13[0] is None else G.dev(cat(s13))
+    S2 = None if s2[0] is None else G.dev(cat(s2))
+    sbytes = lambda s: 0 if s is None else s.nbytes
+    x = rng.standard_normal(H).astype(np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(H)).astype(np.float16)
+    sel = np.array([3, 1], np.int32)
+    prob = np.array([0.7, 0.3], np.float32)
+    ff, y = G.empty(K * EI * 4), G.empty(K * H * 4)
+    d = _lib.GemvDesc()
+    d.wfmt, d.w, d.scales = FMTS[fmt], G.ptr(W13).value, G.ptr(S13).value
+    d.scale_count = 0 if s13[0] is None else s13[0].size
+    d.out_features, d.in_features, d.x, d.x_is_f32 = 2 * EI, H, G.ptr(G.dev(x)).value, 1
+    d.norm_w, d.norm_eps, d.epilogue, d.y = G.ptr(G.dev(nw)).value, 1e-5, _lib.EPI_SWIGLU, G.ptr(ff).value
+    _lib.call("cpi_hip_moe_expert_gemv", ctypes.byref(d), G.ptr(G.dev(sel)), K, E, w13[0].nbytes, sbytes(s13[0]),
+              0, EI * 4, G.stream())
+    d2 = _lib.GemvDesc()
+    d2.wfmt, d2.w, d2.scales = FMTS[fmt], G.ptr(W2).value, G.ptr(S2).value
+    d2.scale_count = 0 if s2[0] is None else s2[0].size
+    d2.out_features, d2.in_features, d2.x, d2.x_is_f32 = H, EI, G.ptr(ff).value, 1
+    d2.epilogue, d2.y = _lib.EPI_STORE_F32, G.ptr(y).value
+    _lib.call("cpi_hip_moe_expert_gemv", ctypes.byref(d2), G.ptr(G.dev(sel)), K, E, w2[0].nbytes, sbytes(s2[0]),
+              EI * 4, H * 4, G.stream())
+    got_ff = G.host(ff, np.float32, K * EI).reshape(K, EI)
+    got_y = G.host(y, np.float32, K * H).reshape(K, H)
+    # the same launches, expert by expert, through the plain GEMV
+    for j, e in enumerate(sel):
+        ffe, ye = G.empty(EI * 4), G.empty(H * 4)
+        G.gemv(FMTS[fmt], G.dev(w13[e]), None if s13[e] is None else G.dev(s13[e]),
+               0 if s13[e] is None else s13[e].size, 2 * EI, H, G.dev(x), ffe, epilogue=_lib.EPI_SWIGLU,
+               norm_w=G.dev(nw), eps=1e-5)
+        np.testing.assert_array_equal(got_ff[j], G.host(ffe, np.float32, EI))
+        G.gemv(FMTS[fmt], G.dev(w2[e]), None if s2[e] is None else G.dev(s2[e]), 0 if s2[e] is None else s2[e].size,
+               H, EI, G.dev(got_ff[j].copy()), ye)
+        np.testing.assert_array_equal(got_y[j], G.host(ye, np.float32, H))
+    base = rng.standard_normal(H).astype(np.float32)
+    xd = G.dev(base)
+    _lib.call("cpi_hip_moe_combine", G.ptr(xd), G.ptr(y), G.ptr(G.dev(prob)), K, H, G.stream())
+    ref = base + (np.float32(0) + prob[0] * got_y[0] + prob[1] * got_y[1])
+    np.testing.assert_allclose(G.host(xd, np.float32, H), ref, rtol=1e-6, atol=1e-6)
