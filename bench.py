@@ -21,22 +21,51 @@ sys.path.insert(0, ROOT)
 PEAK_HBM_GBPS = 8000.0
 PROMPT_LEN, DECODE_LEN = 512, 256
 
+# Named workloads (BASELINE configs 4 and 5): prompt / decode lengths and the
+# algorithmic bytes one decode token streams (weights + scales it reads, KV
+# excluded; the KV term is added per position).
+WORKLOADS = {
+    "llama2-7b": dict(prompt=512, decode=256, file="cpi_llama2_7b_int4g32_L{layers}.ll2c"),
+    "mixtral-8x7b": dict(prompt=256, decode=128, file="cpi_mixtral_8x7b_int4g32_L{layers}.ll2c"),
+}
+
+
+def i4g32_bytes(R, K):
+    return R * K // 2 + R * (K // 32) * 2
+
+
+def token_bytes(workload, layers, pos):
+    """Algorithmic HBM bytes of one decode token at position `pos`."""
+    H, V = 4096, 32000
+    if workload == "llama2-7b":
+        lin = i4g32_bytes(3 * H, H) + i4g32_bytes(H, H) + i4g32_bytes(2 * 11008, H) + i4g32_bytes(H, 11008)
+        kv = 2 * H * 2 * (pos + 1)
+        per_layer = lin + kv + 2 * 2 * H
+    else:
+        kvd, EI = 1024, 14336
+        lin = i4g32_bytes(H + 2 * kvd, H) + i4g32_bytes(H, H) + 2 * (i4g32_bytes(2 * EI, H) + i4g32_bytes(H, EI))
+        kv = 2 * kvd * 2 * (pos + 1)
+        per_layer = lin + kv + 2 * 2 * H + 8 * H * 2
+    return layers * per_layer + V * H * 2 + H * 2
+
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def model_path(layers: int) -> str:
+def model_path(layers: int, workload: str = "llama2-7b") -> str:
     from cpi_amd import ll2c
     import shutil
+    need = (12 << 30) if workload == "llama2-7b" else (34 << 30)
     d = tempfile.gettempdir()
-    if os.path.isdir("/dev/shm") and shutil.disk_usage("/dev/shm").free > (12 << 30):
+    if os.path.isdir("/dev/shm") and shutil.disk_usage("/dev/shm").free > need:
         d = "/dev/shm"
-    p = os.path.join(d, f"cpi_llama2_7b_int4g32_L{layers}.ll2c")
+    p = os.path.join(d, WORKLOADS[workload]["file"].format(layers=layers))
     if not os.path.exists(p):
         t0 = time.time()
-        spec = ll2c.SynthSpec(ll2c.llama2_7b_config(num_layers=layers), attn_fmt="i4g32", mlp_fmt="i4g32",
-                              lm_fmt="f16", seed=0, std=0.02)
+        cfg = (ll2c.llama2_7b_config(num_layers=layers) if workload == "llama2-7b"
+               else ll2c.mixtral_config(num_layers=layers))
+        spec = ll2c.SynthSpec(cfg, attn_fmt="i4g32", mlp_fmt="i4g32", lm_fmt="f16", seed=0, std=0.02)
         ll2c.write_synthetic(p + ".tmp", spec)
         os.replace(p + ".tmp", p)
         log(f"[bench] wrote {p} in {time.time() - t0:.1f}s")
@@ -92,6 +121,8 @@ def main():
     ap.add_argument("--layers", type=int, default=32, help="decoder layers (32 = the benchmark config)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="llama2-7b",
+                    help="llama2-7b = BASELINE config 4 (the headline line); mixtral-8x7b = config 5")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this decode engine runs on one GPU (batch-1 decode, no multi-GPU path); "
@@ -103,6 +134,8 @@ def main():
     from cpi_amd import kbench
     from cpi_amd.engine_py import Engine
 
+    if args.workload != "llama2-7b":
+        return moe_main(args)
     path = model_path(args.layers)
     eng = Engine(path, max_context=PROMPT_LEN + DECODE_LEN + 8, eos=-1, loop_guard=False)
     prompt = np.random.default_rng(0).integers(0, 32000, PROMPT_LEN)
@@ -164,6 +197,57 @@ def main():
         "prefill_gemm_i4g32_m128": pre,
         "roofline": roof,
         "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+def moe_main(args):
+    """Mixtral-8x7B-shaped int4-g32 MoE decode, all experts
+    resident; the roofline line is the whole decode step's algorithmic bytes
+    per token (attention + the two selected experts + lm_head + KV) over the
+    measured time per token."""
+    import numpy as np
+    import torch
+    from cpi_amd.engine_py import Engine
+    w = WORKLOADS[args.workload]
+    path = model_path(args.layers, args.workload)
+    eng = Engine(path, max_context=w["prompt"] + w["decode"] + 8, eos=-1, loop_guard=False)
+    prompt = np.random.default_rng(0).integers(0, 32000, w["prompt"])
+    for _ in range(args.warmup):
+        eng.generate(prompt, w["decode"])
+    torch.cuda.synchronize()
+    decode_ms = prefill_ms = 0.0
+    tokens = 0
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        eng.generate(prompt, w["decode"])
+        s = eng.stats()
+        decode_ms += s["decode_ms"]
+        prefill_ms += s["prefill_ms"]
+        tokens += s["generated_tokens"]
+    wall = time.perf_counter() - t0
+    eng.close()
+    tok_s = tokens / (decode_ms / 1e3)
+    mean_pos = w["prompt"] + w["decode"] // 2
+    tb = token_bytes(args.workload, args.layers, mean_pos)
+    achieved = tb * tok_s / 1e9
+    log(f"[bench] {args.workload}: decode {tokens} tok in {decode_ms:.1f} ms -> {tok_s:.1f} tok/s "
+        f"({tb / 1e9:.2f} GB/token -> {achieved:.0f} GB/s)")
+    out = {
+        "metric": "batch-1 decode tokens/s (Mixtral-8x7B int4 MoE)", "value": round(tok_s, 2), "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 2), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int4-g32 weights, fp16 act/KV, fp32 accumulate", "data": "synthetic",
+        "config": {"workload": "mixtral-8x7b-int4g32-moe-decode", "layers": args.layers, "hidden": 4096,
+                   "heads": 32, "kv_heads": 8, "experts": 8, "top_k": 2, "expert_intermediate": 14336,
+                   "prompt_tokens": w["prompt"], "decode_tokens": w["decode"], "prefill": "sequential",
+                   "parallelism": "single-gpu"},
+        "prefill_tok_per_s": round(args.steps * (w["prompt"] - 1) / (prefill_ms / 1e3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": None,
+                     "kernel": "whole decode step (algorithmic bytes per token / time per token)",
+                     "bytes_per_token": tb},
+        "cpu_baseline": None,
     }
     print(json.dumps(out), flush=True)
 

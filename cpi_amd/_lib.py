@@ -71,6 +71,9 @@ _SIGS = {
     "cpi_hip_attention_prefill_window": (c_int, [c_void_p] * 4 + [c_int] * 6 + [c_void_p]),
     "cpi_hip_prefill_gemm": (c_int, [ctypes.POINTER(GemmDesc), c_void_p]),
     "cpi_hip_rmsnorm_rows_f32": (c_int, [c_void_p] * 3 + [c_int, c_int, c_float, c_void_p]),
+    "cpi_hip_decode_fused_supported": (c_int, [c_void_p]),
+    "cpi_hip_decode_step_fused": (c_int, [c_void_p, c_void_p]),
+    "cpi_hip_decode_fused_status": (c_int, [c_void_p]),
     "cpi_hip_rmsnorm": (c_int, [c_void_p] * 3 + [c_int, c_int, c_float, c_void_p]),
     "cpi_hip_embedding_lookup": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p]),
     "cpi_hip_embedding_lookup_f32": (c_int, [c_void_p] * 3 + [c_int, c_int, c_void_p]),
@@ -93,7 +96,7 @@ _SIGS = {
                                         c_size_t, c_size_t, c_void_p]),
     "cpi_hip_moe_combine": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "cpi_hip_argmax_float": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
-    "cpi_hip_greedy_advance": (c_int, [c_void_p] * 5 + [c_int, c_void_p]),
+    "cpi_hip_greedy_advance": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "cpi_hip_prompt_advance": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "cpi_hip_quantize_rowwise_fp16_to_int8": (c_int, [c_void_p] * 3 + [c_int, c_int, c_int, c_void_p]),
     "cpi_hip_pack_rowwise_int8_to_int4": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),

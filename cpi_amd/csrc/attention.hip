@@ -91,8 +91,22 @@ __device__ __forceinline__ SplitGeom split_geom(const AttnParams& p) {
 // device-scope stores and bumps the KV head's arrival counter; the last
 // workgroup to arrive merges the splits in split order (deterministic) and
 // resets the counter.
-template <int HD, int G, bool QF32, bool OF32>
-__global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
+template <bool OF32, bool COH>
+__device__ __forceinline__ void attn_store_out(void* out, int i, float v) {
+  if constexpr (OF32) {
+    if constexpr (COH) coh_st(static_cast<float*>(out) + i, v);
+    else static_cast<float*>(out)[i] = v;
+  } else {
+    static_cast<uint16_t*>(out)[i] = f2h(v);
+  }
+}
+
+// Work item (kvh, split) of the attention; COH: q is read and the output
+// written with device-coherent accesses (inside a persistent launch that
+// produced q and consumes the output).
+template <int HD, int G, bool QF32, bool OF32, bool COH>
+__device__ __forceinline__ void attn_body(const AttnParams& p, int kvh, int split) {
+  static_assert(!COH || (QF32 && OF32), "coherent mode exchanges fp32 q / out");
   constexpr int LPK = HD / 8;               // lanes per K/V row: 16 B each
   constexpr int NG = kAttnBlock / LPK;      // token groups per workgroup
   constexpr int TB = 4;                     // tokens per group per step
@@ -104,8 +118,6 @@ __global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
   __shared__ float fm[kAttnBlock], fl[kAttnBlock];  // split-merge lane partials
   __shared__ int is_last;
 
-  const int kvh = blockIdx.x;
-  const int split = blockIdx.y;
   const SplitGeom geo = split_geom<CT>(p);
   const int active = geo.active;
   if (split >= active) return;  // uniform per workgroup
@@ -143,14 +155,20 @@ __global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
       const int qi = (kvh * G + g) * HD + cb * 8 + 2 * e;
       float v0, v1;
       if constexpr (QF32) {
-        v0 = static_cast<const float*>(p.q)[qi];
-        v1 = static_cast<const float*>(p.q)[qi + 1];
+        if constexpr (COH) {
+          v0 = coh_ld(static_cast<const float*>(p.q) + qi);
+          v1 = coh_ld(static_cast<const float*>(p.q) + qi + 1);
+        } else {
+          v0 = static_cast<const float*>(p.q)[qi];
+          v1 = static_cast<const float*>(p.q)[qi + 1];
+        }
       } else {
         v0 = h2f(static_cast<const uint16_t*>(p.q)[qi]);
         v1 = h2f(static_cast<const uint16_t*>(p.q)[qi + 1]);
       }
       v0 *= p.scale;
       v1 *= p.scale;
+      asm volatile("" : "+v"(v0), "+v"(v1));  // hi and lo below come from the same fp32 value
       const f16 h0 = static_cast<f16>(v0), h1 = static_cast<f16>(v1);
       qh[g][e] = h2_bits(h0, h1);
       ql[g][e] = h2_bits(static_cast<f16>(v0 - static_cast<float>(h0)), static_cast<f16>(v1 - static_cast<float>(h1)));
@@ -255,15 +273,13 @@ __global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
       }
       const int h = kvh * G + gb + b;
       if (active == 1) {
-        const float r = acc / L;
-        if (OF32) static_cast<float*>(p.out)[h * HD + d] = r;
-        else static_cast<uint16_t*>(p.out)[h * HD + d] = f2h(r);
+        attn_store_out<OF32, COH>(p.out, h * HD + d, acc / L);
       } else {
         const size_t slot = static_cast<size_t>(h) * maxs + split;
-        __hip_atomic_store(&os[slot * HD + d], acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        coh_st(&os[slot * HD + d], acc);
         if (d == 0) {
-          __hip_atomic_store(&ml[slot * 2 + 0], gM[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(&ml[slot * 2 + 1], L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          coh_st(&ml[slot * 2 + 0], gM[b]);
+          coh_st(&ml[slot * 2 + 1], L);
         }
       }
     }
@@ -294,7 +310,7 @@ __global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
   constexpr int CPT = HD > TPH ? HD / TPH : 1;    // columns per thread
   constexpr int SUB = TPH > HD ? TPH / HD : 1;    // split lanes per column
   constexpr int MAXJ = CPT <= 2 ? 16 : 8;
-  auto ld = [](const float* a) { return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  auto ld = [](const float* a) { return coh_ld(a); };
   const int g = tid / TPH;
   const int r = tid % TPH;
   const int h = kvh * G + g;
@@ -337,9 +353,7 @@ __global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
   if constexpr (SUB == 1) {
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-      const float res = acc[c] / Lt;
-      if (OF32) static_cast<float*>(p.out)[h * HD + c0 + c] = res;
-      else static_cast<uint16_t*>(p.out)[h * HD + c0 + c] = f2h(res);
+      attn_store_out<OF32, COH>(p.out, h * HD + c0 + c, acc[c] / Lt);
     }
   } else {
     // combine the SUB split lanes of each column (CPT == 1 here)
@@ -360,11 +374,14 @@ __global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
         L = fmaf(fl[tid + q * HD], w, L);
         o2 = fmaf(fo[tid + q * HD], w, o2);
       }
-      const float res = o2 / L;
-      if (OF32) static_cast<float*>(p.out)[h * HD + c0] = res;
-      else static_cast<uint16_t*>(p.out)[h * HD + c0] = f2h(res);
+      attn_store_out<OF32, COH>(p.out, h * HD + c0, o2 / L);
     }
   }
+}
+
+template <int HD, int G, bool QF32, bool OF32>
+__global__ void __launch_bounds__(kAttnBlock) attn_kernel(AttnParams p) {
+  attn_body<HD, G, QF32, OF32, false>(p, blockIdx.x, blockIdx.y);
 }
 
 namespace {

@@ -13,6 +13,7 @@
 #include "attention.hip"
 #include "ops.hip"
 #include "prefill.hip"
+#include "decode_fused.hip"
 
 namespace {
 
@@ -371,8 +372,10 @@ int cpi_hip_moe_router(const float* x, const uint16_t* norm_w, float eps, const 
   if (!x || !norm_w || !router_w || !idx || !prob) return fail("moe_router: null pointer");
   if (experts <= 0 || experts > 64 || top_k <= 0 || top_k > experts)
     return fail("moe_router: experts must be in [1, 64] and 1 <= top_k <= experts");
-  if (hidden <= 0 || hidden > 256 * cpi::kRouterMaxPer) return fail("moe_router: hidden must be in [1, 8192]");
-  hipLaunchKernelGGL(cpi::moe_router_kernel, dim3(1), dim3(256), 0, S(s), x, norm_w, eps, router_w, experts, hidden,
+  if (hidden <= 0 || hidden > cpi::kRouterMaxHidden || hidden % 8 != 0)
+    return fail("moe_router: hidden must be a multiple of 8 in [8, 8192]");
+  if ((reinterpret_cast<uintptr_t>(router_w) & 15) != 0) return fail("moe_router: router_w must be 16-byte aligned");
+  hipLaunchKernelGGL(cpi::moe_router_kernel, dim3(1), dim3(cpi::kRouterThreads), 0, S(s), x, norm_w, eps, router_w, experts, hidden,
                      top_k, idx, prob, logits_out);
   return check(hipGetLastError(), "moe_router");
 }
@@ -515,6 +518,71 @@ int cpi_hip_prefill_gemm(const cpi_gemm_desc* d, cpi_stream_t s) {
     p.max_ctx = d->max_context;
   }
   return check(cpi::pgemm_launch(d->wfmt, p, S(s)), "prefill_gemm");
+}
+
+int cpi_hip_decode_fused_supported(const cpi_fused_decode_desc* d) {
+  if (!d) return fail("decode_fused: null descriptor") == 0;
+  const char* why = nullptr;
+  if (!cpi::fused_supported(*d, &why)) {
+    fail(std::string("decode_fused: ") + why);
+    return 0;
+  }
+  return 1;
+}
+
+int cpi_hip_decode_step_fused(const cpi_fused_decode_desc* d, cpi_stream_t s) {
+  if (!d) return fail("decode_fused: null descriptor");
+  const char* why = nullptr;
+  if (!cpi::fused_supported(*d, &why)) return fail(std::string("decode_fused: ") + why);
+  if (!d->layers || d->num_layers <= 0 || !d->embedding || !d->norm_out || !d->lm_head || !d->rope_cos ||
+      !d->rope_sin || !d->x || !d->q || !d->att || !d->ff || !d->logits || !d->attn_scratch || !d->token ||
+      !d->position || !d->step || !d->ring || d->ring_len <= 0 || !d->sync)
+    return fail("decode_fused: null pointer in descriptor");
+  if ((reinterpret_cast<uintptr_t>(d->sync) & 7) != 0) return fail("decode_fused: sync must be 8-byte aligned");
+  const int gq = d->num_heads / d->num_kv_heads;
+  const int maxw = cpi::fused_max_wgs(d->head_dim, gq);
+  if (maxw <= 0) return fail("decode_fused: occupancy query failed");
+  int wgs = d->workgroups > 0 ? d->workgroups : maxw;
+  if (wgs > maxw) return fail("decode_fused: more workgroups than fit on the device at once");
+  cpi::FusedParams P{};
+  P.layers = d->layers;
+  P.nlayers = d->num_layers;
+  P.H = d->hidden;
+  P.I = d->intermediate;
+  P.V = d->vocab;
+  P.nh = d->num_heads;
+  P.nkv = d->num_kv_heads;
+  P.hd = d->head_dim;
+  P.max_ctx = d->max_context;
+  P.window = d->sliding_window;
+  P.nsplit = cpi::attn_num_splits(d->num_kv_heads);
+  P.eps = d->norm_eps;
+  P.attn_scale = 1.4426950408889634f / sqrtf(static_cast<float>(d->head_dim));
+  P.emb = d->embedding;
+  P.norm_out = d->norm_out;
+  P.lm_w = d->lm_head;
+  P.rope_cos = d->rope_cos;
+  P.rope_sin = d->rope_sin;
+  P.x = d->x;
+  P.q = d->q;
+  P.att = d->att;
+  P.ff = d->ff;
+  P.logits = d->logits;
+  P.attn_scratch = d->attn_scratch;
+  P.token = d->token;
+  P.pos = d->position;
+  P.step = d->step;
+  P.ring = d->ring;
+  P.ring_len = d->ring_len;
+  P.sync = d->sync;
+  P.spin_limit = 1 << 20;
+  return check(cpi::fused_launch(P, d->head_dim, gq, wgs, S(s)), "decode_fused");
+}
+
+int cpi_hip_decode_fused_status(const uint32_t* sync_host) {
+  if (!sync_host) return fail("decode_fused_status: null pointer");
+  if (sync_host[cpi::kSyncAbort] != 0) return fail("decode_fused: a device-wide barrier timed out (workgroups not co-resident?)");
+  return 0;
 }
 
 int cpi_hip_rmsnorm_rows_f32(const float* x, const uint16_t* w, uint16_t* y, int rows, int cols, float eps,

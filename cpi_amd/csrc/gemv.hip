@@ -88,8 +88,27 @@ enum { EPI_DUAL_F16 = 100 };
 // ---------------------------------------------------------------------------
 // Activation preparation (one chunk).
 // ---------------------------------------------------------------------------
+// The prepared form feeds a bias-compensated dot (sum h*a minus a per-chunk
+// constant built from the same a, with h ~ 1024): the constant and the stored
+// fp16 values must come from bit-identical inputs, or a one-ulp difference
+// becomes ~1024 ulps in the row sum.  With fp contraction the compiler may
+// fold the producer's fp32 multiply into one fp16 conversion (single rounding)
+// and not into another use of the same value (double rounding), so the fp32
+// inputs are materialised once here before any conversion.
+template <int N>
+__device__ __forceinline__ void pin_floats(const float* in, float* out) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    out[i] = in[i];
+    asm volatile("" : "+v"(out[i]));
+  }
+}
+
 template <int FMT>
-__device__ __forceinline__ void prep_chunk(const float* v, uint32_t* dst) {
+__device__ __forceinline__ void prep_chunk(const float* v_in, uint32_t* dst) {
+  constexpr int N = FMT == CPI_W_F16 ? 8 : (FMT == CPI_W_I8ROW ? 16 : 32);
+  float v[N];
+  pin_floats<N>(v_in, v);
   if constexpr (FMT == CPI_W_F16) {
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
@@ -191,7 +210,9 @@ __device__ __forceinline__ void unit_floats(const XUnit<XF32>& r, float* v) {
 // Prepared form of unit d of a chunk (same values and layout as prep_chunk);
 // returns the unit's share of the chunk's bias sum.
 template <int FMT>
-__device__ __forceinline__ float prep_unit(const float* v, uint32_t* dst, int d) {
+__device__ __forceinline__ float prep_unit(const float* v_in, uint32_t* dst, int d) {
+  float v[8];
+  pin_floats<8>(v_in, v);
   if constexpr (FMT == CPI_W_F16) {
     prep_chunk<FMT>(v, dst);
     return 0.f;
@@ -688,7 +709,8 @@ hipError_t launch_shape(const GemvParams& p, int epi, const GemvPlan& g, size_t 
 
 template <int FMT, bool XF32>
 hipError_t launch(const GemvParams& p, int epi, hipStream_t s) {
-  const GemvPlan g = plan_launch(p.R, p.K, FmtT<FMT>::kElems, g_force_shape, g_force_ks);
+  const GemvPlan g = plan_launch(p.R, p.K, FmtT<FMT>::kElems, g_force_shape, g_force_ks,
+                                 p.expert_idx != nullptr ? p.num_slots : 1);
   const size_t lds = lds_bytes<FMT>(p.K);
   if (lds > 160 * 1024) return hipErrorInvalidValue;  // K too large for the LDS plan
   static_assert(kNumShapes == 6, "shape table and dispatch must agree");

@@ -82,8 +82,9 @@ CPI_HD inline bool plan_valid(int shape, int ks) {
 
 // Host plan: all loads of a wave in flight at once where the shape allows,
 // full pass utilisation, and enough waves (>= 2 per SIMD of 256 CUs) to fill
-// the chip.  force_shape / force_ks (>= 0 / > 0) override the choice.
-inline GemvPlan plan_launch(int R, int K, int elems, int force_shape, int force_ks) {
+// the chip; `slots` launches of the plan run side by side (grid.y, gathered
+// MoE experts).  force_shape / force_ks (>= 0 / > 0) override the choice.
+inline GemvPlan plan_launch(int R, int K, int elems, int force_shape, int force_ks, int slots = 1) {
   double best = -1.0;
   GemvPlan bp = make_plan(R, K, elems, 0, 1);
   for (int s = 0; s < kNumShapes; ++s) {
@@ -93,7 +94,7 @@ inline GemvPlan plan_launch(int R, int K, int elems, int force_shape, int force_
       if (!plan_valid(s, ks)) continue;
       const GemvPlan g = make_plan(R, K, elems, s, ks);
       const double util = static_cast<double>(g.np) / (static_cast<double>(g.ks) * g.ng * g.pp);
-      const double waves = static_cast<double>(g.grid) * kWavesPerBlock;
+      const double waves = static_cast<double>(g.grid) * kWavesPerBlock * slots;
       double score = util * (waves >= 2048.0 ? 1.0 : waves / 2048.0);
       if (g.ng > 1) score *= 0.9;
       if (g.nr * g.pp < 8) score *= 0.9;

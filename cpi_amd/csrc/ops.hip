@@ -143,38 +143,66 @@ __global__ void router_topk_kernel(const uint16_t* logits, int experts, int top_
 //      cpu_engine.cpp:392-405 order), router logits against fp16 router rows
 //      [experts, hidden] in fp32, then the top-k softmax above — the router
 //      matvec + moe_router_topk_softmax of llama_engine_forward_decode.cpp:
-//      395-426 as one launch with no host round trip.  One block of 256.
-constexpr int kRouterMaxPer = 32;  // hidden <= 256 * 32
-__global__ void __launch_bounds__(256) moe_router_kernel(const float* x, const uint16_t* norm_w, float eps,
-                                                         const uint16_t* rw, int experts, int hidden, int top_k,
-                                                         int* idx, float* prob, float* logits_out) {
-  __shared__ float red[4];
+//      395-426 as one launch with no host round trip.  One block of 8 waves:
+//      the normalised activations go to LDS, then wave w dots router rows
+//      w, w+8, ... with 16-byte loads.
+constexpr int kRouterThreads = 512;
+constexpr int kRouterMaxHidden = 8192;
+constexpr int kRouterRowLoads = kRouterMaxHidden / 8 / 64;  // 16-byte loads per lane per router row
+__global__ void __launch_bounds__(kRouterThreads) moe_router_kernel(const float* x, const uint16_t* norm_w, float eps,
+                                                                    const uint16_t* rw, int experts, int hidden,
+                                                                    int top_k, int* idx, float* prob,
+                                                                    float* logits_out) {
+  __shared__ float red[kRouterThreads / 64];
   __shared__ float lg[64];
-  float xn[kRouterMaxPer];
-  float ss = 0.f;
+  __shared__ __align__(16) float xn[kRouterMaxHidden];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nc = hidden / 8;  // 16-byte chunks per router row
+  // the first router row of this wave is requested before anything else
+  u32x4 rr[kRouterRowLoads];
+  if (wave < experts) {
+    const uint16_t* r = rw + static_cast<size_t>(wave) * hidden;
 #pragma unroll
-  for (int j = 0; j < kRouterMaxPer; ++j) {
-    const int i = threadIdx.x + 256 * j;
-    xn[j] = i < hidden ? x[i] : 0.f;
-    ss += xn[j] * xn[j];
+    for (int j = 0; j < kRouterRowLoads; ++j) {
+      const int c = min(lane + 64 * j, nc - 1);
+      rr[j] = *reinterpret_cast<const u32x4*>(r + 8 * c);
+    }
+  }
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < hidden; i += kRouterThreads) {
+    const float v = x[i];
+    xn[i] = v;
+    ss += v * v;
   }
   ss = block_sum(ss, red);
   const float inv = 1.f / sqrtf(ss / static_cast<float>(hidden) + eps);
-#pragma unroll
-  for (int j = 0; j < kRouterMaxPer; ++j) {
-    const int i = threadIdx.x + 256 * j;
-    xn[j] = i < hidden ? inv * xn[j] * h2f(norm_w[i]) : 0.f;
-  }
-  for (int e = 0; e < experts; ++e) {
-    const uint16_t* r = rw + static_cast<size_t>(e) * hidden;
+  for (int i = threadIdx.x; i < hidden; i += kRouterThreads) xn[i] = inv * xn[i] * h2f(norm_w[i]);
+  __syncthreads();
+  auto dot_chunk = [&](const u32x4 w8, int c) {
+    const uint32_t wd[4] = {w8.x, w8.y, w8.z, w8.w};
     float d = 0.f;
 #pragma unroll
-    for (int j = 0; j < kRouterMaxPer; ++j) {
-      const int i = threadIdx.x + 256 * j;
-      if (i < hidden) d += xn[j] * h2f(r[i]);
+    for (int q = 0; q < 4; ++q) {
+      const f16x2 h = as_h2(wd[q]);
+      d += xn[8 * c + 2 * q] * static_cast<float>(h.x);
+      d += xn[8 * c + 2 * q + 1] * static_cast<float>(h.y);
     }
-    d = block_sum(d, red);
-    if (threadIdx.x == 0) lg[e] = d;
+    return d;
+  };
+  for (int e = wave; e < experts; e += kRouterThreads / 64) {
+    float d = 0.f;
+    if (e == wave) {
+#pragma unroll
+      for (int j = 0; j < kRouterRowLoads; ++j) {
+        const int c = lane + 64 * j;
+        if (c < nc) d += dot_chunk(rr[j], c);
+      }
+    } else {
+      const uint16_t* r = rw + static_cast<size_t>(e) * hidden;
+      for (int c = lane; c < nc; c += 64) d += dot_chunk(*reinterpret_cast<const u32x4*>(r + 8 * c), c);
+    }
+    d = wave_sum(d);
+    if (lane == 0) lg[e] = d;
   }
   __syncthreads();
   if (threadIdx.x == 0) {

@@ -390,12 +390,13 @@ void LlamaEngine::initialize(const EngineOptions& options) {
   }
   HIP_OK(hipDeviceSynchronize());
 
+  setup_fused();
   build_graphs();
   if (opts_.verbose) {
     std::cout << "[engine] resident gfx950 decode: layers=" << NL << " hidden=" << H << " heads=" << NH
               << " kv_heads=" << NKV << " head_dim=" << head_dim_ << " inter=" << I << " vocab=" << V
               << " max_context=" << opts_.max_context << " rope_theta=" << theta_
-              << " prefill_chunk=" << prefill_chunk_
+              << " prefill_chunk=" << prefill_chunk_ << " fused_decode=" << (fused_ ? 1 : 0)
               << " weights_mb=" << (weight_bytes_ >> 20) << "\n";
     std::cout << "[startup] phase=initialize ms=" << ms_since(t0) << "\n";
   }
@@ -403,8 +404,62 @@ void LlamaEngine::initialize(const EngineOptions& options) {
 
 // One token: embedding -> L x (QKV+RoPE+KV store, attention, o_proj+residual,
 // w1|w3+SwiGLU, w2+residual) -> [final norm + lm_head + argmax/advance].
+void LlamaEngine::setup_fused() {
+  fused_ = false;
+  // opt-in: on MI355X a device-wide barrier currently costs more than the
+  // kernel boundary it replaces, so the per-op graph stays the default
+  const char* env = std::getenv("CPI_FUSED_DECODE");
+  if (!env || std::string(env) != "1") return;
+  if (cfg_.is_moe() || lm_head_.wfmt != CPI_W_F16) return;
+  for (const auto& L : layers_)
+    if (L.qkv.wfmt != CPI_W_I4G32 || L.wo.wfmt != CPI_W_I4G32 || L.w13.wfmt != CPI_W_I4G32 ||
+        L.w2.wfmt != CPI_W_I4G32)
+      return;
+  std::vector<cpi_fused_layer> table(layers_.size());
+  for (std::size_t l = 0; l < layers_.size(); ++l) {
+    const Layer& L = layers_[l];
+    cpi_fused_layer& f = table[l];
+    f.wqkv = L.qkv.w; f.sqkv = L.qkv.scales; f.wo = L.wo.w; f.so = L.wo.scales;
+    f.w13 = L.w13.w; f.s13 = L.w13.scales; f.w2 = L.w2.w; f.s2 = L.w2.scales;
+    f.norm_att = L.norm_att; f.norm_ffn = L.norm_ffn; f.k_cache = L.k_cache; f.v_cache = L.v_cache;
+  }
+  cpi_fused_decode_desc& d = fused_desc_;
+  d = cpi_fused_decode_desc{};
+  d.num_layers = static_cast<int>(layers_.size());
+  d.hidden = cfg_.hidden_size; d.intermediate = cfg_.intermediate_size; d.vocab = cfg_.vocab_size;
+  d.num_heads = cfg_.num_heads; d.num_kv_heads = cfg_.num_kv_heads; d.head_dim = head_dim_;
+  d.max_context = opts_.max_context; d.sliding_window = cfg_.sliding_window; d.norm_eps = cfg_.norm_eps;
+  d.embedding = emb_; d.norm_out = norm_out_; d.lm_head = static_cast<const uint16_t*>(lm_head_.w);
+  d.rope_cos = rope_cos_; d.rope_sin = rope_sin_;
+  d.x = x_; d.q = q_; d.att = att_; d.ff = ff_; d.logits = logits_; d.attn_scratch = attn_scratch_;
+  d.token = d_token_; d.position = d_pos_; d.step = d_step_; d.ring = d_ring_; d.ring_len = ring_len_;
+  if (const char* env = std::getenv("CPI_FUSED_WORKGROUPS")) d.workgroups = std::atoi(env);
+  if (!cpi_hip_decode_fused_supported(&d)) {
+    if (opts_.verbose) std::cout << "[engine] fused decode off: " << cpi_hip_last_error_string() << "\n";
+    return;
+  }
+  auto* dt = static_cast<cpi_fused_layer*>(dmalloc(table.size() * sizeof(cpi_fused_layer)));
+  HIP_OK(hipMemcpy(dt, table.data(), table.size() * sizeof(cpi_fused_layer), hipMemcpyHostToDevice));
+  d.layers = dt;
+  d_sync_ = static_cast<uint32_t*>(dmalloc(64));
+  HIP_OK(hipMemset(d_sync_, 0, 64));
+  d.sync = d_sync_;
+  fused_ = true;
+}
+
+void LlamaEngine::check_fused() const {
+  if (!fused_) return;
+  uint32_t s[16];
+  HIP_OK(hipMemcpy(s, d_sync_, sizeof(s), hipMemcpyDeviceToHost));
+  if (cpi_hip_decode_fused_status(s) != 0) ENGINE_THROW(cpi_hip_last_error_string());
+}
+
 void LlamaEngine::enqueue_step(bool with_head) {
   const int H = cfg_.hidden_size, I = cfg_.intermediate_size;
+  if (with_head && fused_) {
+    CPI_OK(cpi_hip_decode_step_fused(&fused_desc_, stream_));
+    return;
+  }
   CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_token_, x_, 1, H, stream_));
   for (auto& L : layers_) {
     cpi_gemv_desc d{};
@@ -544,6 +599,7 @@ void LlamaEngine::reset_state(const std::vector<int>& prompt) {
   HIP_OK(hipMemcpyAsync(d_token_, &first, 4, hipMemcpyHostToDevice, stream_));
   HIP_OK(hipMemcpyAsync(d_pos_, &zero, 4, hipMemcpyHostToDevice, stream_));
   HIP_OK(hipMemcpyAsync(d_step_, &zero, 4, hipMemcpyHostToDevice, stream_));
+  if (fused_) HIP_OK(hipMemsetAsync(d_sync_, 0, 64, stream_));  // barrier counters restart at zero
   HIP_OK(hipStreamSynchronize(stream_));
 }
 
@@ -621,6 +677,7 @@ std::vector<int> LlamaEngine::generate_stream(const std::vector<int>& prompt_in,
   }
   HIP_OK(hipStreamSynchronize(stream_));
   stats_.decode_ms = ms_since(td);
+  check_fused();
   return out;
 }
 

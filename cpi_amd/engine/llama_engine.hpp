@@ -14,6 +14,7 @@
 #include <utility>
 #include <vector>
 
+#include "cpi_hip.h"
 #include "ll2c_file.hpp"
 
 namespace engine {
@@ -192,6 +193,14 @@ class LlamaEngine {
   hipGraphExec_t g_decode_many_ = nullptr, g_decode_one_ = nullptr;
   hipGraphExec_t g_prefill_many_ = nullptr, g_prefill_one_ = nullptr;
   int graph_steps_ = 16;
+
+  // fused persistent decode step (one launch per token) when the model is a
+  // dense all-int4-g32 Llama; otherwise the per-op graph
+  bool fused_ = false;
+  cpi_fused_decode_desc fused_desc_{};
+  uint32_t* d_sync_ = nullptr;
+  void setup_fused();
+  void check_fused() const;
 
   // chunked prefill (MFMA GEMMs): residual [C, H] fp32, GEMM inputs fp16
   int prefill_chunk_ = 1;

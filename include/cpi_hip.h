@@ -244,6 +244,61 @@ typedef struct cpi_gemm_desc {
 
 int cpi_hip_prefill_gemm(const cpi_gemm_desc* d, cpi_stream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Fused decode step: one persistent launch per token runs the embedding, all
+ * layers, the final norm + lm_head and the greedy advance (argmax -> token,
+ * ring[*step % ring_len] = token, ++*step, ++*position), i.e. the whole
+ * token of the reference's captured decode graph
+ * (src/engine/llama_engine_graph.cpp:166-480) in one kernel with device-wide
+ * barriers between dependent phases.  Dense Llama layers, every linear
+ * CPI_W_I4G32 in the engine's fused row orders (cpi_hip_qkv_row_order,
+ * cpi_hip_swiglu_row_order), fp16 embeddings / norms / lm_head.
+ * ---------------------------------------------------------------------- */
+typedef struct cpi_fused_layer {
+  const void* wqkv; const void* sqkv;   /* int4 [qkv_rows, H/2], fp16 [qkv_rows, H/32] */
+  const void* wo; const void* so;       /* [H, qdim/2], [H, qdim/32] */
+  const void* w13; const void* s13;     /* [2I, H/2], [2I, H/32] */
+  const void* w2; const void* s2;       /* [H, I/2], [H, I/32] */
+  const uint16_t* norm_att;
+  const uint16_t* norm_ffn;
+  uint16_t* k_cache;                    /* [max_context, kv_dim] fp16 */
+  uint16_t* v_cache;
+} cpi_fused_layer;
+
+typedef struct cpi_fused_decode_desc {
+  const cpi_fused_layer* layers;        /* DEVICE array [num_layers] */
+  int num_layers, hidden, intermediate, vocab;
+  int num_heads, num_kv_heads, head_dim, max_context, sliding_window;
+  float norm_eps;
+  const uint16_t* embedding;            /* [vocab, hidden] */
+  const uint16_t* norm_out;             /* [hidden] */
+  const uint16_t* lm_head;              /* [vocab, hidden] fp16 */
+  const float* rope_cos;                /* [max_context, head_dim/2] */
+  const float* rope_sin;
+  float* x;                             /* [hidden] */
+  float* q;                             /* [num_heads*head_dim] */
+  float* att;                           /* [num_heads*head_dim] */
+  float* ff;                            /* [intermediate] */
+  float* logits;                        /* [vocab], written every step */
+  float* attn_scratch;                  /* cpi_hip_attention_scratch_floats() */
+  int* token;
+  int* position;
+  int* step;
+  int* ring;
+  int ring_len;
+  uint32_t* sync;                       /* 16 words, zero before first use and
+                                           after a reported failure */
+  int workgroups;                       /* 0 = all that fit on the device */
+} cpi_fused_decode_desc;
+
+/* 1 when the shapes / formats are served by the fused step, else 0 (and
+ * cpi_hip_last_error_string() says why). */
+int cpi_hip_decode_fused_supported(const cpi_fused_decode_desc* d);
+int cpi_hip_decode_step_fused(const cpi_fused_decode_desc* d, cpi_stream_t stream);
+/* Host check after the launches have completed: 0, or -1 when a device-wide
+ * barrier timed out (sync_host = the 16 sync words copied to the host). */
+int cpi_hip_decode_fused_status(const uint32_t* sync_host);
+
 /* Row RMSNorm of the fp32 residual stream into fp16 GEMM input:
  * y[r, :] = fp16((x[r, :] * rsqrt(mean(x[r, :]^2) + eps)) * w) — the
  * launch_norm of prefill_prompt (llama_engine.cpp:626-653) for fp32 rows. */
@@ -312,7 +367,8 @@ int cpi_hip_moe_router_topk_softmax(const uint16_t* logits, int experts,
  * (fp16 [experts, hidden], fp32 accumulate), softmax over experts, greedy
  * top-k with strict '>' and renormalisation (kernels_ops_matvec.cu:115-193).
  * topk_idx int [top_k], topk_prob fp32 [top_k]; logits_out fp32 [experts] or
- * NULL.  experts <= 64, hidden <= 8192. */
+ * NULL.  experts <= 64, hidden a multiple of 8 up to 8192, router_w 16-byte
+ * aligned. */
 int cpi_hip_moe_router(const float* x, const uint16_t* norm_w, float eps,
                        const uint16_t* router_w, int experts, int hidden,
                        int top_k, int* topk_idx, float* topk_prob,

@@ -122,6 +122,56 @@ def test_chunked_prefill_matches_sequential(tmp_path, name):
         np.sort(rl)[-1] - np.sort(rl)[-2] <= 4 * LOGIT_TOL
 
 
+FUSED_CASES = {
+    "mha_hd128": tiny_cfg(hidden_size=512, num_heads=4, num_kv_heads=4, intermediate_size=1024),
+    "gqa4_hd64": tiny_cfg(hidden_size=512, num_heads=8, num_kv_heads=2, intermediate_size=1408),
+    "gqa8_hd64_window": tiny_cfg(hidden_size=512, num_heads=8, num_kv_heads=1, intermediate_size=768,
+                                 sliding_window=24, rope_theta=500000.0),
+}
+
+
+@pytest.mark.parametrize("name", list(FUSED_CASES))
+def test_fused_decode_matches_graph_and_oracle(tmp_path, name, monkeypatch):
+    """The persistent one-launch-per-token decode (all-int4-g32 models) gives
+    the per-op graph's ids and logits, and the oracle's within the bar."""
+    from cpi_amd.engine_py import Engine
+    cfg = FUSED_CASES[name]
+    print(f"[fused] case={name}", flush=True)
+    path = str(tmp_path / f"{name}.ll2c")
+    ll2c.write_synthetic(path, ll2c.SynthSpec(cfg, attn_fmt="i4g32", mlp_fmt="i4g32", lm_fmt="f16", seed=4,
+                                              std=0.02, norm_jitter=0.1))
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab_size, 29)
+    out = {}
+    for fused in ("1", "0"):
+        monkeypatch.setenv("CPI_FUSED_DECODE", fused)
+        eng = Engine(path, max_context=96, eos=-1, loop_guard=False, verbose=True)
+        ids, lg = eng.generate(prompt, 40, logit_steps=40)
+        ids16, _ = eng.generate(prompt, 48)  # 16-step graph launches
+        out[fused] = (ids, lg, ids16)
+        eng.close()
+    ref = oracle.Engine(path, 96)
+    rids, rlg = ref.generate(prompt, 40, eos=-1, logit_steps=40)
+    (fi, fl, f16), (gi, gl, g16) = out["1"], out["0"]
+    n = first_divergence(fi, gi)
+    d = np.abs(fl[:n] - gl[:n]).max()
+    no = first_divergence(fi, rids)
+    err = np.abs(fl[:no] - rlg[:no]).max()
+    ng = first_divergence(gi, rids)
+    gerr = np.abs(gl[:ng] - rlg[:ng]).max()
+    per_step = np.abs(fl[:no] - rlg[:no]).max(1)
+    print(f"[fused] {name} fused-vs-graph max_abs={d:.3e} prefix={n}/40; vs oracle err={err:.3e} "
+          f"prefix={no}/40 (graph vs oracle {gerr:.3e}) {margin_note(rlg, no)}", flush=True)
+    print(f"[fused] {name} per-step fused err: {np.array2string(per_step[:12], precision=4)}", flush=True)
+    # same activation rounding, different fp32 summation order of the int4
+    # offset-binary dots (partial sums ~1024x the result): ~1e-4 per dot,
+    # a few 1e-3 in the logits after the layers
+    assert d <= 2e-2
+    assert n == 40 or np.sort(gl[n - 1])[-1] - np.sort(gl[n - 1])[-2] <= 4 * max(d, 1e-6)
+    assert err <= LOGIT_TOL
+    assert_ids_or_tie(no, rlg, err)
+    assert (f16[:40] == fi).all()
+
+
 def test_engine_eos_and_empty_prompt(tmp_path):
     from cpi_amd.engine_py import Engine
     cfg = tiny_cfg()
