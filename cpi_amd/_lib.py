@@ -27,7 +27,7 @@ class GemvDesc(ctypes.Structure):
         ("norm_w", c_void_p), ("norm_eps", c_float), ("epilogue", c_int), ("y", c_void_p),
         ("num_heads", c_int), ("num_kv_heads", c_int), ("head_dim", c_int), ("position", c_void_p),
         ("rope_cos", c_void_p), ("rope_sin", c_void_p), ("k_cache", c_void_p), ("v_cache", c_void_p),
-        ("max_context", c_int),
+        ("max_context", c_int), ("add_y", c_void_p), ("add_p", c_void_p), ("add_k", c_int), ("x_out", c_void_p),
     ]
 
 
@@ -44,7 +44,7 @@ class GemmDesc(ctypes.Structure):
 
 
 W_F16, W_I8ROW, W_I4ROW, W_I4G32 = 0, 1, 2, 3
-EPI_STORE_F32, EPI_STORE_F16, EPI_RESID_ADD, EPI_SWIGLU, EPI_QKV_ROPE = 0, 1, 2, 3, 4
+EPI_STORE_F32, EPI_STORE_F16, EPI_RESID_ADD, EPI_SWIGLU, EPI_QKV_ROPE, EPI_SWIGLU_F16 = 0, 1, 2, 3, 4, 5
 ATTN_MAX_SPLITS = 256
 
 # name -> (restype, argtypes)

@@ -105,7 +105,7 @@ __device__ __forceinline__ void attn_store_out(void* out, int i, float v) {
 // written with device-coherent accesses (inside a persistent launch that
 // produced q and consumes the output).
 template <int HD, int G, bool QF32, bool OF32, bool COH>
-__device__ __forceinline__ void attn_body(const AttnParams& p, int kvh, int split) {
+__device__ __forceinline__ void attn_body(const AttnParams p, int kvh, int split) {
   static_assert(!COH || (QF32 && OF32), "coherent mode exchanges fp32 q / out");
   constexpr int LPK = HD / 8;               // lanes per K/V row: 16 B each
   constexpr int NG = kAttnBlock / LPK;      // token groups per workgroup
@@ -168,7 +168,6 @@ __device__ __forceinline__ void attn_body(const AttnParams& p, int kvh, int spli
       }
       v0 *= p.scale;
       v1 *= p.scale;
-      asm volatile("" : "+v"(v0), "+v"(v1));  // hi and lo below come from the same fp32 value
       const f16 h0 = static_cast<f16>(v0), h1 = static_cast<f16>(v1);
       qh[g][e] = h2_bits(h0, h1);
       ql[g][e] = h2_bits(static_cast<f16>(v0 - static_cast<float>(h0)), static_cast<f16>(v1 - static_cast<float>(h1)));

@@ -140,7 +140,7 @@ static int gemv_params(const cpi_gemv_desc* d, cpi::GemvParams& p) {
   p.norm_w = d->norm_w;
   p.eps = d->norm_eps;
   p.y = d->y;
-  if (d->epilogue == CPI_EPI_SWIGLU && (d->out_features % 8) != 0)
+  if ((d->epilogue == CPI_EPI_SWIGLU || d->epilogue == CPI_EPI_SWIGLU_F16) && (d->out_features % 8) != 0)
     return fail("gemv: SWIGLU needs out_features (= 2 x intermediate) % 8 == 0");
   if (d->epilogue == CPI_EPI_QKV_ROPE) {
     if (d->head_dim % 8 != 0 || d->num_heads <= 0 || d->num_kv_heads <= 0)
@@ -159,8 +159,20 @@ static int gemv_params(const cpi_gemv_desc* d, cpi::GemvParams& p) {
     p.v_cache = d->v_cache;
     p.max_ctx = d->max_context;
   }
-  if (d->epilogue < CPI_EPI_STORE_F32 || d->epilogue > CPI_EPI_QKV_ROPE)
+  if (d->epilogue < CPI_EPI_STORE_F32 || d->epilogue > CPI_EPI_SWIGLU_F16)
     return fail("gemv: unknown epilogue");
+  if (d->add_k != 0) {
+    if (d->add_k < 0 || d->add_k > 2 || !d->add_y || !d->add_p)
+      return fail("gemv: add_k must be 0, 1 or 2 with add_y and add_p");
+    if (!d->x_is_f32 || d->in_features > 4096)
+      return fail("gemv: the folded residual update needs fp32 x and in_features <= 4096");
+    if ((reinterpret_cast<uintptr_t>(d->add_y) | reinterpret_cast<uintptr_t>(d->x_out)) & 15)
+      return fail("gemv: add_y and x_out must be 16-byte aligned");
+    p.add_y = d->add_y;
+    p.add_p = d->add_p;
+    p.add_k = d->add_k;
+    p.x_out = d->x_out;
+  }
   return 0;
 }
 

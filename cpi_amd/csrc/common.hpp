@@ -51,22 +51,21 @@ __device__ __forceinline__ float group_sum(float v) {
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
 
 // Device-coherent accesses for data exchanged between workgroups of one
-// launch.  The XCDs' L2 caches are not coherent with each other, and an
-// agent-scope access (sc1) may still be served by a line this XCD's L2 holds
-// from an earlier read, so these use system scope (sc0 sc1): stores write
-// through to memory and loads are never served from L2.  A writer makes its
-// stores visible by waiting for them (s_waitcnt vmcnt(0)) before it signals.
+// launch: relaxed agent-scope atomics (sc1), which the memory model keeps
+// coherent across all XCDs of the device (their L2 caches are not coherent
+// for ordinary accesses).  A writer makes its stores visible by waiting for
+// them (s_waitcnt vmcnt(0)) before it signals.
 __device__ __forceinline__ float coh_ld(const float* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void coh_st(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint32_t coh_ld_u32(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void coh_st_u32(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ float wave_max(float v) {

@@ -81,6 +81,13 @@ struct GemvParams {
   const int* expert_idx;
   int num_experts, num_slots;
   size_t w_estride, s_estride, x_sstride, y_sstride;
+  // Residual update folded into the prologue (MoE combine): the input is
+  // x + sum_{j < add_k} add_p[j] * add_y[j * K + :] (fp32 x, add_k <= 2,
+  // K <= 4096); workgroup (0, 0) writes that input to x_out when non-null.
+  const float* add_y;
+  const float* add_p;
+  int add_k;
+  float* x_out;
 };
 
 enum { EPI_DUAL_F16 = 100 };
@@ -89,74 +96,66 @@ enum { EPI_DUAL_F16 = 100 };
 // Activation preparation (one chunk).
 // ---------------------------------------------------------------------------
 // The prepared form feeds a bias-compensated dot (sum h*a minus a per-chunk
-// constant built from the same a, with h ~ 1024): the constant and the stored
-// fp16 values must come from bit-identical inputs, or a one-ulp difference
-// becomes ~1024 ulps in the row sum.  With fp contraction the compiler may
-// fold the producer's fp32 multiply into one fp16 conversion (single rounding)
-// and not into another use of the same value (double rounding), so the fp32
-// inputs are materialised once here before any conversion.
-template <int N>
-__device__ __forceinline__ void pin_floats(const float* in, float* out) {
-#pragma unroll
-  for (int i = 0; i < N; ++i) {
-    out[i] = in[i];
-    asm volatile("" : "+v"(out[i]));
-  }
+// constant built from the same a, with h ~ 1024): the constant must be built
+// from exactly the fp16 bits that are stored, or a one-ulp difference becomes
+// ~1024 ulps in the row sum.  With fp contraction the compiler may produce one
+// use of a converted value by a single-rounding multiply-convert and another
+// by multiply-then-convert, so each packed pair word is pinned once and every
+// later use (the store and the bias sums) is read back from that word.
+__device__ __forceinline__ uint32_t pin_word(uint32_t w) {
+  asm volatile("" : "+v"(w));
+  return w;
+}
+__device__ __forceinline__ float lo_f(uint32_t w) { return static_cast<float>(as_h2(w).x); }
+__device__ __forceinline__ float hi_f(uint32_t w) { return static_cast<float>(as_h2(w).y); }
+
+// One unit (8 values) of the int4 prepared form: four pair words and the
+// unit's share of the chunk bias.  Low nibbles pair with a = x (h = 1024 +
+// n'), high nibbles with a = x/16 (h = 1024 + 16 n'); sum(q x) = sum(h a) -
+// [1024 sum(a) + 8 sum(x~)] with x~ = 16 a on high lanes.
+__device__ __forceinline__ float prep_i4_unit(const float* e, uint32_t* out) {
+  const uint32_t w0 = pin_word(h2_bits(static_cast<f16>(e[0]), static_cast<f16>(e[4])));
+  const uint32_t w1 = pin_word(h2_bits(static_cast<f16>(e[1] * 0.0625f), static_cast<f16>(e[5] * 0.0625f)));
+  const uint32_t w2 = pin_word(h2_bits(static_cast<f16>(e[2]), static_cast<f16>(e[6])));
+  const uint32_t w3 = pin_word(h2_bits(static_cast<f16>(e[3] * 0.0625f), static_cast<f16>(e[7] * 0.0625f)));
+  out[0] = w0;
+  out[1] = w1;
+  out[2] = w2;
+  out[3] = w3;
+  const float lo = (lo_f(w0) + hi_f(w0)) + (lo_f(w2) + hi_f(w2));
+  const float hi = (lo_f(w1) + hi_f(w1)) + (lo_f(w3) + hi_f(w3));
+  return 1024.f * (lo + hi) + 8.f * (lo + 16.f * hi);
+}
+
+// Four values of the int8 prepared form (byte b' = q + 128 under 1024.0,
+// h = 1152 + q): two pair words and their activation sum.
+__device__ __forceinline__ float prep_i8_quad(const float* v, uint32_t* out) {
+  const uint32_t w0 = pin_word(h2_bits(static_cast<f16>(v[0]), static_cast<f16>(v[2])));
+  const uint32_t w1 = pin_word(h2_bits(static_cast<f16>(v[1]), static_cast<f16>(v[3])));
+  out[0] = w0;
+  out[1] = w1;
+  return (lo_f(w0) + lo_f(w1)) + (hi_f(w0) + hi_f(w1));
 }
 
 template <int FMT>
-__device__ __forceinline__ void prep_chunk(const float* v_in, uint32_t* dst) {
-  constexpr int N = FMT == CPI_W_F16 ? 8 : (FMT == CPI_W_I8ROW ? 16 : 32);
-  float v[N];
-  pin_floats<N>(v_in, v);
+__device__ __forceinline__ void prep_chunk(const float* v, uint32_t* dst) {
   if constexpr (FMT == CPI_W_F16) {
+    // hi/lo split: the lo part is computed from the stored hi bits
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
-      const f16 h0 = static_cast<f16>(v[2 * d]);
-      const f16 h1 = static_cast<f16>(v[2 * d + 1]);
-      const f16 l0 = static_cast<f16>(v[2 * d] - static_cast<float>(h0));
-      const f16 l1 = static_cast<f16>(v[2 * d + 1] - static_cast<float>(h1));
-      dst[d] = h2_bits(h0, h1);
-      dst[4 + d] = h2_bits(l0, l1);
+      const uint32_t hw = pin_word(h2_bits(static_cast<f16>(v[2 * d]), static_cast<f16>(v[2 * d + 1])));
+      dst[d] = hw;
+      dst[4 + d] = h2_bits(static_cast<f16>(v[2 * d] - lo_f(hw)), static_cast<f16>(v[2 * d + 1] - hi_f(hw)));
     }
   } else if constexpr (FMT == CPI_W_I8ROW) {
-    // byte b' = q + 128 sits under 1024.0:  h = 1152 + q.
     float asum = 0.f;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const f16 a0 = static_cast<f16>(v[4 * d + 0]);
-      const f16 a1 = static_cast<f16>(v[4 * d + 1]);
-      const f16 a2 = static_cast<f16>(v[4 * d + 2]);
-      const f16 a3 = static_cast<f16>(v[4 * d + 3]);
-      dst[2 * d + 0] = h2_bits(a0, a2);
-      dst[2 * d + 1] = h2_bits(a1, a3);
-      asum += (static_cast<float>(a0) + static_cast<float>(a1)) +
-              (static_cast<float>(a2) + static_cast<float>(a3));
-    }
+    for (int d = 0; d < 4; ++d) asum += prep_i8_quad(v + 4 * d, dst + 2 * d);
     dst[8] = __builtin_bit_cast(uint32_t, -1152.f * asum);
   } else {
-    // nibble n' = q + 8.  Low nibbles: h = 1024 + n', paired with a = x.
-    // High nibbles: h = 1024 + 16 n', paired with a = x/16.
-    // sum h*a = 1024*sum(a) + sum(n' * x~) with x~ = 16a on high lanes, so
-    // sum(q x~) = sum(h a) - [1024*sum(a) + 8*sum(x~)].
     float c = 0.f;
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      const float* e = v + 8 * d;
-      const f16 p0 = static_cast<f16>(e[0]), p4 = static_cast<f16>(e[4]);
-      const f16 p1 = static_cast<f16>(e[1] * 0.0625f), p5 = static_cast<f16>(e[5] * 0.0625f);
-      const f16 p2 = static_cast<f16>(e[2]), p6 = static_cast<f16>(e[6]);
-      const f16 p3 = static_cast<f16>(e[3] * 0.0625f), p7 = static_cast<f16>(e[7] * 0.0625f);
-      dst[4 * d + 0] = h2_bits(p0, p4);
-      dst[4 * d + 1] = h2_bits(p1, p5);
-      dst[4 * d + 2] = h2_bits(p2, p6);
-      dst[4 * d + 3] = h2_bits(p3, p7);
-      const float lo = (static_cast<float>(p0) + static_cast<float>(p4)) +
-                       (static_cast<float>(p2) + static_cast<float>(p6));
-      const float hi = (static_cast<float>(p1) + static_cast<float>(p5)) +
-                       (static_cast<float>(p3) + static_cast<float>(p7));
-      c += 1024.f * (lo + hi) + 8.f * (lo + 16.f * hi);
-    }
+    for (int d = 0; d < 4; ++d) c += prep_i4_unit(v + 8 * d, dst + 4 * d);
     dst[16] = __builtin_bit_cast(uint32_t, -c);
   }
 }
@@ -210,41 +209,14 @@ __device__ __forceinline__ void unit_floats(const XUnit<XF32>& r, float* v) {
 // Prepared form of unit d of a chunk (same values and layout as prep_chunk);
 // returns the unit's share of the chunk's bias sum.
 template <int FMT>
-__device__ __forceinline__ float prep_unit(const float* v_in, uint32_t* dst, int d) {
-  float v[8];
-  pin_floats<8>(v_in, v);
+__device__ __forceinline__ float prep_unit(const float* v, uint32_t* dst, int d) {
   if constexpr (FMT == CPI_W_F16) {
     prep_chunk<FMT>(v, dst);
     return 0.f;
   } else if constexpr (FMT == CPI_W_I8ROW) {
-    float asum = 0.f;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const f16 a0 = static_cast<f16>(v[4 * h + 0]);
-      const f16 a1 = static_cast<f16>(v[4 * h + 1]);
-      const f16 a2 = static_cast<f16>(v[4 * h + 2]);
-      const f16 a3 = static_cast<f16>(v[4 * h + 3]);
-      dst[4 * d + 2 * h + 0] = h2_bits(a0, a2);
-      dst[4 * d + 2 * h + 1] = h2_bits(a1, a3);
-      asum += (static_cast<float>(a0) + static_cast<float>(a1)) +
-              (static_cast<float>(a2) + static_cast<float>(a3));
-    }
-    return asum;
+    return prep_i8_quad(v, dst + 4 * d) + prep_i8_quad(v + 4, dst + 4 * d + 2);
   } else {
-    const float* e = v;
-    const f16 p0 = static_cast<f16>(e[0]), p4 = static_cast<f16>(e[4]);
-    const f16 p1 = static_cast<f16>(e[1] * 0.0625f), p5 = static_cast<f16>(e[5] * 0.0625f);
-    const f16 p2 = static_cast<f16>(e[2]), p6 = static_cast<f16>(e[6]);
-    const f16 p3 = static_cast<f16>(e[3] * 0.0625f), p7 = static_cast<f16>(e[7] * 0.0625f);
-    dst[4 * d + 0] = h2_bits(p0, p4);
-    dst[4 * d + 1] = h2_bits(p1, p5);
-    dst[4 * d + 2] = h2_bits(p2, p6);
-    dst[4 * d + 3] = h2_bits(p3, p7);
-    const float lo = (static_cast<float>(p0) + static_cast<float>(p4)) +
-                     (static_cast<float>(p2) + static_cast<float>(p6));
-    const float hi = (static_cast<float>(p1) + static_cast<float>(p5)) +
-                     (static_cast<float>(p3) + static_cast<float>(p7));
-    return 1024.f * (lo + hi) + 8.f * (lo + 16.f * hi);
+    return prep_i4_unit(v, dst + 4 * d);
   }
 }
 
@@ -400,12 +372,16 @@ __device__ __forceinline__ void row_epilogue(const GemvParams& p, int epi, int r
       else static_cast<uint16_t*>(p.y2)[row - p.rows_a] = f2h(acc);
       break;
     case CPI_EPI_RESID_ADD: static_cast<float*>(p.y)[row] += acc; break;
-    case CPI_EPI_SWIGLU: {
+    case CPI_EPI_SWIGLU:
+    case CPI_EPI_SWIGLU_F16: {
       // tile T rows: [w1 4T..4T+3 | w3 4T..4T+3]
       const int r = row % kTileRows;
       if (r < 4) {
         const float u = fin[t + 4];
-        static_cast<float*>(p.y)[(row / kTileRows) * 4 + r] = (acc / (1.f + expf(-acc))) * u;
+        const float v = (acc / (1.f + expf(-acc))) * u;
+        const int i = (row / kTileRows) * 4 + r;
+        if (epi == CPI_EPI_SWIGLU) static_cast<float*>(p.y)[i] = v;
+        else static_cast<uint16_t*>(p.y)[i] = f2h(v);
       }
       break;
     }
@@ -453,9 +429,10 @@ __device__ __forceinline__ void row_epilogue(const GemvParams& p, int epi, int r
 // segments.  Per group a wave issues NR x PP 16-byte loads per lane (clamped
 // in-bounds addresses), then consumes them pass by pass.
 // ---------------------------------------------------------------------------
-template <int FMT, bool XF32, int NR, int PP, int MAXU>
+template <int FMT, bool XF32, int NR, int PP, int MAXU, bool FOLD, bool GATHER>
 __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int epi, int ks) {
-  if (p.expert_idx != nullptr) {
+  static_assert(!FOLD || (XF32 && MAXU <= 2), "the folded residual update needs fp32 x held in registers");
+  if constexpr (GATHER) {
     int e = __builtin_amdgcn_readfirstlane(p.expert_idx[blockIdx.y]);
     e = e < 0 ? 0 : (e >= p.num_experts ? p.num_experts - 1 : e);
     p.w = static_cast<const uint8_t*>(p.w) + static_cast<size_t>(e) * p.w_estride;
@@ -501,6 +478,23 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int epi, int
       nv[k] = *reinterpret_cast<const u32x4*>(nsrc + 8 * u);
     }
   }
+  // expert outputs to fold into x: requested with the activations, ahead of
+  // the weights (vmcnt counts in order, so waiting for them later does not
+  // drain the weight stream)
+  XUnit<true> yv[2][FOLD ? MAXU : 1];
+  const int add_k = (FOLD && in_regs) ? p.add_k : 0;
+  if constexpr (FOLD) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (j < add_k) {
+#pragma unroll
+        for (int k = 0; k < MAXU; ++k) {
+          const int u = min(static_cast<int>(threadIdx.x) + k * kBlock, nunits - 1);
+          yv[j][k] = load_unit<true>(p.add_y + static_cast<size_t>(j) * K, u);
+        }
+      }
+    }
+  }
 
   // ---- group-0 weight loads: issued behind the activation loads, so waiting
   // for the activations (vmcnt = number of weight loads) leaves them in flight
@@ -530,6 +524,38 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int epi, int
     for (int k = 0; k < MAXU; ++k) {
       pin_unit<XF32>(xv[k]);
       asm volatile("" : "+v"(nv[k]));
+    }
+    if constexpr (FOLD) {
+      if (add_k > 0) {
+        // x + (p0 y0 + p1 y1), the order of cpi_hip_moe_combine
+        const float p0 = p.add_p[0];
+        const float p1 = add_k > 1 ? p.add_p[1] : 0.f;
+#pragma unroll
+        for (int k = 0; k < MAXU; ++k) {
+          pin_unit<true>(yv[0][k]);
+          float xs[8], y0[8], y1[8];
+          unit_floats<true>(xv[k], xs);
+          unit_floats<true>(yv[0][k], y0);
+          if (add_k > 1) {
+            pin_unit<true>(yv[1][k]);
+            unit_floats<true>(yv[1][k], y1);
+          }
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float acc = fmaf(p0, y0[e], 0.f);
+            if (add_k > 1) acc = fmaf(p1, y1[e], acc);
+            xs[e] += acc;
+          }
+          xv[k].a = f32x4{xs[0], xs[1], xs[2], xs[3]};
+          xv[k].b = f32x4{xs[4], xs[5], xs[6], xs[7]};
+          const int u = static_cast<int>(threadIdx.x) + k * kBlock;
+          if (p.x_out != nullptr && blockIdx.x == 0 && blockIdx.y == 0 && u < nunits) {
+            f32x4* o = reinterpret_cast<f32x4*>(p.x_out + 8 * u);
+            o[0] = xv[k].a;
+            o[1] = xv[k].b;
+          }
+        }
+      }
     }
     float inv_rms = 1.f;
     if (has_norm) {
@@ -685,17 +711,17 @@ size_t lds_bytes(int K) {
   return static_cast<size_t>(K / FmtT<FMT>::kElems) * FmtT<FMT>::kStride * sizeof(uint32_t);
 }
 
-template <int FMT, bool XF32, int NR, int PP, int MAXU>
+template <int FMT, bool XF32, int NR, int PP, int MAXU, bool FOLD = false, bool GATHER = false>
 hipError_t launch_kernel(const GemvParams& p, int epi, const GemvPlan& g, size_t lds, hipStream_t s) {
   static size_t lds_set = 0;  // per instantiation: raise the dynamic-LDS limit once
   if (lds > 64 * 1024 && lds > lds_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<FMT, XF32, NR, PP, MAXU>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<FMT, XF32, NR, PP, MAXU, FOLD, GATHER>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return e;
     lds_set = lds;
   }
-  const int slots = p.expert_idx != nullptr ? p.num_slots : 1;
-  hipLaunchKernelGGL((gemv_kernel<FMT, XF32, NR, PP, MAXU>), dim3(g.grid, slots), dim3(kBlock), lds, s, p, epi, g.ks);
+  const int slots = GATHER ? p.num_slots : 1;
+  hipLaunchKernelGGL((gemv_kernel<FMT, XF32, NR, PP, MAXU, FOLD, GATHER>), dim3(g.grid, slots), dim3(kBlock), lds, s, p, epi, g.ks);
   return hipGetLastError();
 }
 
@@ -703,6 +729,13 @@ hipError_t launch_kernel(const GemvParams& p, int epi, const GemvPlan& g, size_t
 // K <= 16384; larger K takes the strided path.
 template <int FMT, bool XF32, int NR, int PP>
 hipError_t launch_shape(const GemvParams& p, int epi, const GemvPlan& g, size_t lds, hipStream_t s) {
+  if constexpr (XF32) {
+    if (p.add_k > 0) return launch_kernel<FMT, XF32, NR, PP, 2, true>(p, epi, g, lds, s);
+  }
+  if (p.expert_idx != nullptr) {
+    if (p.K <= 2 * 8 * kBlock) return launch_kernel<FMT, XF32, NR, PP, 2, false, true>(p, epi, g, lds, s);
+    return launch_kernel<FMT, XF32, NR, PP, 8, false, true>(p, epi, g, lds, s);
+  }
   if (p.K <= 2 * 8 * kBlock) return launch_kernel<FMT, XF32, NR, PP, 2>(p, epi, g, lds, s);
   return launch_kernel<FMT, XF32, NR, PP, 8>(p, epi, g, lds, s);
 }
@@ -729,7 +762,7 @@ template <int FMT>
 hipError_t dispatch_x(int epi, bool xf32, const GemvParams& p, hipStream_t s) {
   switch (epi) {
     case CPI_EPI_STORE_F32: case CPI_EPI_STORE_F16: case CPI_EPI_RESID_ADD:
-    case CPI_EPI_SWIGLU: case CPI_EPI_QKV_ROPE: case EPI_DUAL_F16: break;
+    case CPI_EPI_SWIGLU: case CPI_EPI_SWIGLU_F16: case CPI_EPI_QKV_ROPE: case EPI_DUAL_F16: break;
     default: return hipErrorInvalidValue;
   }
   return xf32 ? launch<FMT, true>(p, epi, s) : launch<FMT, false>(p, epi, s);

@@ -168,15 +168,28 @@ __global__ void __launch_bounds__(kRouterThreads) moe_router_kernel(const float*
       rr[j] = *reinterpret_cast<const u32x4*>(r + 8 * c);
     }
   }
-  float ss = 0.f;
-  for (int i = threadIdx.x; i < hidden; i += kRouterThreads) {
-    const float v = x[i];
-    xn[i] = v;
-    ss += v * v;
+  // every activation and norm weight this thread needs, requested at once
+  constexpr int kPer = kRouterMaxHidden / kRouterThreads;
+  float xv[kPer];
+  uint16_t nv[kPer];
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = threadIdx.x + j * kRouterThreads;
+    const int ic = i < hidden ? i : hidden - 1;
+    xv[j] = x[ic];
+    nv[j] = norm_w[ic];
   }
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < kPer; ++j)
+    if (threadIdx.x + j * kRouterThreads < hidden) ss += xv[j] * xv[j];
   ss = block_sum(ss, red);
   const float inv = 1.f / sqrtf(ss / static_cast<float>(hidden) + eps);
-  for (int i = threadIdx.x; i < hidden; i += kRouterThreads) xn[i] = inv * xn[i] * h2f(norm_w[i]);
+#pragma unroll
+  for (int j = 0; j < kPer; ++j) {
+    const int i = threadIdx.x + j * kRouterThreads;
+    if (i < hidden) xn[i] = inv * xv[j] * h2f(nv[j]);
+  }
   __syncthreads();
   auto dot_chunk = [&](const u32x4 w8, int c) {
     const uint32_t wd[4] = {w8.x, w8.y, w8.z, w8.w};
@@ -217,8 +230,10 @@ __global__ void __launch_bounds__(kRouterThreads) moe_router_kernel(const float*
 __global__ void moe_combine_kernel(float* x, const float* y, const float* prob, int top_k, int hidden) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= hidden) return;
+  // explicit fma chain: the GEMV prologue that folds this update computes the
+  // identical sequence (independent of fp contraction)
   float acc = 0.f;
-  for (int k = 0; k < top_k; ++k) acc += prob[k] * y[static_cast<size_t>(k) * hidden + i];
+  for (int k = 0; k < top_k; ++k) acc = fmaf(prob[k], y[static_cast<size_t>(k) * hidden + i], acc);
   x[i] += acc;
 }
 

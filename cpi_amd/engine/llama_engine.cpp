@@ -351,6 +351,10 @@ void LlamaEngine::initialize(const EngineOptions& options) {
     d_moe_prob_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(moe_top_k_) * 4));
     moe_ff_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(moe_top_k_) * moe_inter_ * 4));
     moe_y_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(moe_top_k_) * H * 4));
+    // the combine folds into the next GEMV prologue when it can (<= 2 experts,
+    // hidden <= 4096); residuals then alternate between x_ and x2_
+    moe_fold_ = moe_top_k_ <= 2 && H <= 4096 && !(std::getenv("CPI_MOE_COMBINE") && std::string(std::getenv("CPI_MOE_COMBINE")) == "1");
+    if (moe_fold_) x2_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(H) * 4));
   }
   logits_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(V) * 4));
   attn_scratch_ = static_cast<float*>(dmalloc(cpi_hip_attention_scratch_floats(NH, head_dim_) * 4));
@@ -390,6 +394,7 @@ void LlamaEngine::initialize(const EngineOptions& options) {
   }
   HIP_OK(hipDeviceSynchronize());
 
+  f32_handoff_ = std::getenv("CPI_F32_HANDOFF") && std::string(std::getenv("CPI_F32_HANDOFF")) == "1";
   setup_fused();
   build_graphs();
   if (opts_.verbose) {
@@ -461,65 +466,93 @@ void LlamaEngine::enqueue_step(bool with_head) {
     return;
   }
   CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_token_, x_, 1, H, stream_));
+  // MoE layers leave their expert outputs (moe_y_, weights d_moe_prob_) to be
+  // folded into the next consumer's prologue, which writes the updated
+  // residual to the other buffer of the x_ / x2_ pair.
+  float* cur = x_;
+  bool pending = false;
+  auto fold = [&](cpi_gemv_desc& d, bool write_out) {
+    if (!pending) return;
+    d.add_y = moe_y_;
+    d.add_p = d_moe_prob_;
+    d.add_k = moe_top_k_;
+    if (write_out) {
+      cur = cur == x_ ? x2_ : x_;
+      d.x_out = cur;
+    }
+    pending = false;
+  };
   for (auto& L : layers_) {
     cpi_gemv_desc d{};
     d.wfmt = L.qkv.wfmt; d.w = L.qkv.w; d.scales = L.qkv.scales; d.scale_count = L.qkv.scale_count;
     d.out_features = L.qkv.rows; d.in_features = H;
-    d.x = x_; d.x_is_f32 = 1; d.norm_w = L.norm_att; d.norm_eps = cfg_.norm_eps;
+    d.x = cur; d.x_is_f32 = 1; d.norm_w = L.norm_att; d.norm_eps = cfg_.norm_eps;
     d.epilogue = CPI_EPI_QKV_ROPE; d.y = q_;
     d.num_heads = cfg_.num_heads; d.num_kv_heads = cfg_.num_kv_heads; d.head_dim = head_dim_;
     d.position = d_pos_; d.rope_cos = rope_cos_; d.rope_sin = rope_sin_;
     d.k_cache = L.k_cache; d.v_cache = L.v_cache; d.max_context = opts_.max_context;
+    fold(d, true);
     CPI_OK(cpi_hip_gemv(&d, stream_));
 
-    CPI_OK(cpi_hip_attention_decode(q_, 1, L.k_cache, L.v_cache, att_, 1, 0, d_pos_, cfg_.num_heads,
+    // int4 / int8 consumers round their input to fp16 in the prologue, so
+    // the producer hands over fp16 (half the bytes every workgroup re-reads);
+    // fp16 weights keep fp32 input for their hi/lo split
+    const int att_f32 = (L.wo.wfmt == CPI_W_F16 || f32_handoff_) ? 1 : 0;
+    CPI_OK(cpi_hip_attention_decode(q_, 1, L.k_cache, L.v_cache, att_, att_f32, 0, d_pos_, cfg_.num_heads,
                                     cfg_.num_kv_heads, head_dim_, opts_.max_context, cfg_.sliding_window,
                                     attn_scratch_, stream_));
 
     cpi_gemv_desc o{};
     o.wfmt = L.wo.wfmt; o.w = L.wo.w; o.scales = L.wo.scales; o.scale_count = L.wo.scale_count;
-    o.out_features = H; o.in_features = q_dim_; o.x = att_; o.x_is_f32 = 1;
-    o.epilogue = CPI_EPI_RESID_ADD; o.y = x_;
+    o.out_features = H; o.in_features = q_dim_; o.x = att_; o.x_is_f32 = att_f32;
+    o.epilogue = CPI_EPI_RESID_ADD; o.y = cur;
     CPI_OK(cpi_hip_gemv(&o, stream_));
 
     if (L.moe) {
-      // router + top-k on device, both selected experts in one launch each,
-      // then x += sum_k p_k y_k
-      CPI_OK(cpi_hip_moe_router(x_, L.norm_ffn, cfg_.norm_eps, static_cast<const uint16_t*>(L.router.w),
+      // router + top-k on device, both selected experts in one launch each;
+      // x += sum_k p_k y_k happens in the next prologue (or the combine kernel)
+      CPI_OK(cpi_hip_moe_router(cur, L.norm_ffn, cfg_.norm_eps, static_cast<const uint16_t*>(L.router.w),
                                 moe_experts_, H, moe_top_k_, d_moe_idx_, d_moe_prob_, nullptr, stream_));
       const int EI = moe_inter_;
       cpi_gemv_desc g{};
       g.wfmt = L.ew13.wfmt; g.w = L.ew13.w; g.scales = L.ew13.scales; g.scale_count = L.ew13.scale_count;
-      g.out_features = 2 * EI; g.in_features = H; g.x = x_; g.x_is_f32 = 1;
-      g.norm_w = L.norm_ffn; g.norm_eps = cfg_.norm_eps; g.epilogue = CPI_EPI_SWIGLU; g.y = moe_ff_;
+      g.out_features = 2 * EI; g.in_features = H; g.x = cur; g.x_is_f32 = 1;
+      const bool ff16 = L.ew2.wfmt != CPI_W_F16;
+      const std::size_t ff_slot = static_cast<std::size_t>(EI) * (ff16 ? 2 : 4);
+      g.norm_w = L.norm_ffn; g.norm_eps = cfg_.norm_eps; g.y = moe_ff_;
+      g.epilogue = ff16 ? CPI_EPI_SWIGLU_F16 : CPI_EPI_SWIGLU;
       CPI_OK(cpi_hip_moe_expert_gemv(&g, d_moe_idx_, moe_top_k_, moe_experts_, L.ew13_w_stride, L.ew13_s_stride, 0,
-                                     static_cast<std::size_t>(EI) * 4, stream_));
+                                     ff_slot, stream_));
       cpi_gemv_desc w{};
       w.wfmt = L.ew2.wfmt; w.w = L.ew2.w; w.scales = L.ew2.scales; w.scale_count = L.ew2.scale_count;
-      w.out_features = H; w.in_features = EI; w.x = moe_ff_; w.x_is_f32 = 1;
+      w.out_features = H; w.in_features = EI; w.x = moe_ff_; w.x_is_f32 = ff16 ? 0 : 1;
       w.epilogue = CPI_EPI_STORE_F32; w.y = moe_y_;
       CPI_OK(cpi_hip_moe_expert_gemv(&w, d_moe_idx_, moe_top_k_, moe_experts_, L.ew2_w_stride, L.ew2_s_stride,
-                                     static_cast<std::size_t>(EI) * 4, static_cast<std::size_t>(H) * 4, stream_));
-      CPI_OK(cpi_hip_moe_combine(x_, moe_y_, d_moe_prob_, moe_top_k_, H, stream_));
+                                     ff_slot, static_cast<std::size_t>(H) * 4, stream_));
+      if (moe_fold_) pending = true;
+      else CPI_OK(cpi_hip_moe_combine(cur, moe_y_, d_moe_prob_, moe_top_k_, H, stream_));
       continue;
     }
     cpi_gemv_desc g{};
     g.wfmt = L.w13.wfmt; g.w = L.w13.w; g.scales = L.w13.scales; g.scale_count = L.w13.scale_count;
-    g.out_features = 2 * I; g.in_features = H; g.x = x_; g.x_is_f32 = 1;
-    g.norm_w = L.norm_ffn; g.norm_eps = cfg_.norm_eps; g.epilogue = CPI_EPI_SWIGLU; g.y = ff_;
+    g.out_features = 2 * I; g.in_features = H; g.x = cur; g.x_is_f32 = 1;
+    const int ff_f32 = (L.w2.wfmt == CPI_W_F16 || f32_handoff_) ? 1 : 0;
+    g.norm_w = L.norm_ffn; g.norm_eps = cfg_.norm_eps; g.y = ff_;
+    g.epilogue = ff_f32 ? CPI_EPI_SWIGLU : CPI_EPI_SWIGLU_F16;
     CPI_OK(cpi_hip_gemv(&g, stream_));
 
     cpi_gemv_desc w{};
     w.wfmt = L.w2.wfmt; w.w = L.w2.w; w.scales = L.w2.scales; w.scale_count = L.w2.scale_count;
-    w.out_features = H; w.in_features = I; w.x = ff_; w.x_is_f32 = 1;
-    w.epilogue = CPI_EPI_RESID_ADD; w.y = x_;
+    w.out_features = H; w.in_features = I; w.x = ff_; w.x_is_f32 = ff_f32;
+    w.epilogue = CPI_EPI_RESID_ADD; w.y = cur;
     CPI_OK(cpi_hip_gemv(&w, stream_));
   }
   if (with_head) {
     cpi_gemv_desc h{};
     h.wfmt = lm_head_.wfmt; h.w = lm_head_.w; h.scales = lm_head_.scales; h.scale_count = lm_head_.scale_count;
-    h.out_features = cfg_.vocab_size; h.in_features = H; h.x = x_; h.x_is_f32 = 1;
+    h.out_features = cfg_.vocab_size; h.in_features = H; h.x = cur; h.x_is_f32 = 1;
     h.norm_w = norm_out_; h.norm_eps = cfg_.norm_eps; h.epilogue = CPI_EPI_STORE_F32; h.y = logits_;
+    fold(h, false);
     CPI_OK(cpi_hip_gemv(&h, stream_));
     CPI_OK(cpi_hip_greedy_advance(logits_, cfg_.vocab_size, d_token_, d_pos_, d_step_, d_ring_, ring_len_,
                                   stream_));

@@ -184,6 +184,9 @@ class LlamaEngine {
   int moe_experts_ = 0, moe_top_k_ = 0, moe_inter_ = 0;
   int* d_moe_idx_ = nullptr;
   float *d_moe_prob_ = nullptr, *moe_ff_ = nullptr, *moe_y_ = nullptr;
+  float* x2_ = nullptr;     // second residual buffer (MoE combine folded into the next prologue)
+  bool moe_fold_ = false;
+  bool f32_handoff_ = false;  // CPI_F32_HANDOFF=1: fp32 activations between GEMVs (A/B)
   int *d_token_ = nullptr, *d_pos_ = nullptr, *d_step_ = nullptr, *d_ring_ = nullptr,
       *d_prompt_ = nullptr;
   int ring_len_ = 16;

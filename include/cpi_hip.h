@@ -110,7 +110,9 @@ enum {
   CPI_EPI_STORE_F16 = 1,
   CPI_EPI_RESID_ADD = 2,
   CPI_EPI_SWIGLU = 3,
-  CPI_EPI_QKV_ROPE = 4
+  CPI_EPI_QKV_ROPE = 4,
+  CPI_EPI_SWIGLU_F16 = 5  /* as CPI_EPI_SWIGLU, y fp16: for a consumer whose
+                             int4/int8 prologue rounds x to fp16 anyway */
 };
 
 typedef struct cpi_gemv_desc {
@@ -134,6 +136,15 @@ typedef struct cpi_gemv_desc {
   uint16_t* k_cache;      /* this layer's [max_ctx, kv_dim] fp16 */
   uint16_t* v_cache;
   int max_context;
+  /* Optional residual update folded into the prologue (the MoE combine of
+   * the previous layer): the input becomes
+   *   x + (add_p[0] * add_y[0:K] + add_p[1] * add_y[K:2K])   (add_k terms)
+   * and, when x_out != NULL, that sum is also written to x_out [K].
+   * add_k in {0, 1, 2}; needs x_is_f32 and in_features <= 4096. */
+  const float* add_y;     /* device fp32 [add_k, in_features] */
+  const float* add_p;     /* device fp32 [add_k] */
+  int add_k;
+  float* x_out;
 } cpi_gemv_desc;
 
 int cpi_hip_gemv(const cpi_gemv_desc* d, cpi_stream_t stream);

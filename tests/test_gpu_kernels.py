@@ -382,3 +382,28 @@ def test_moe_expert_gemv_and_combine(fmt):
     _lib.call("cpi_hip_moe_combine", G.ptr(xd), G.ptr(y), G.ptr(G.dev(prob)), K, H, G.stream())
     ref = base + (np.float32(0) + prob[0] * got_y[0] + prob[1] * got_y[1])
     np.testing.assert_allclose(G.host(xd, np.float32, H), ref, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("add_k", [1, 2])
+def test_gemv_folded_moe_residual(add_k):
+    """x + sum_j p_j y_j folded into the GEMV prologue equals cpi_hip_moe_combine
+    followed by the plain GEMV, and x_out receives the combined residual."""
+    R, K = 1024, 4096
+    rng = np.random.default_rng(40 + add_k)
+    blob, sc, _ = make_weights("i4g32", R, K, 77, random_lowbit=True)
+    x = rng.standard_normal(K).astype(np.float32)
+    y = rng.standard_normal((2, K)).astype(np.float32)
+    pr = np.array([0.6, 0.4], np.float32)
+    nw = (1 + 0.1 * rng.standard_normal(K)).astype(np.float16)
+    w, s, yd, pd, nd = G.dev(blob), G.dev(sc), G.dev(y), G.dev(pr), G.dev(nw)
+    # reference: combine, then GEMV
+    xr = G.dev(x)
+    _lib.call("cpi_hip_moe_combine", G.ptr(xr), G.ptr(yd), G.ptr(pd), add_k, K, G.stream())
+    ref = G.empty(R * 4)
+    G.gemv(_lib.W_I4G32, w, s, sc.size, R, K, xr, ref, norm_w=nd)
+    # folded
+    xo = G.empty(K * 4)
+    got = G.empty(R * 4)
+    G.gemv(_lib.W_I4G32, w, s, sc.size, R, K, G.dev(x), got, norm_w=nd, add_y=yd, add_p=pd, add_k=add_k, x_out=xo)
+    np.testing.assert_array_equal(G.host(xo, np.float32, K), G.host(xr, np.float32, K))
+    np.testing.assert_array_equal(G.host(got, np.float32, R), G.host(ref, np.float32, R))
