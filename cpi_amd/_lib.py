@@ -40,12 +40,14 @@ class GemmDesc(ctypes.Structure):
         ("num_heads", c_int), ("num_kv_heads", c_int), ("head_dim", c_int), ("start_position", c_int),
         ("rope_cos", c_void_p), ("rope_sin", c_void_p), ("k_cache", c_void_p), ("v_cache", c_void_p),
         ("max_context", c_int),
+        ("workspace", c_void_p), ("workspace_bytes", c_size_t),
     ]
 
 
 W_F16, W_I8ROW, W_I4ROW, W_I4G32 = 0, 1, 2, 3
 EPI_STORE_F32, EPI_STORE_F16, EPI_RESID_ADD, EPI_SWIGLU, EPI_QKV_ROPE, EPI_SWIGLU_F16 = 0, 1, 2, 3, 4, 5
 ATTN_MAX_SPLITS = 256
+PREFILL_COUNTER_BYTES = 16384
 
 # name -> (restype, argtypes)
 _SIGS = {
@@ -70,6 +72,7 @@ _SIGS = {
     "cpi_hip_attention_prefill": (c_int, [c_void_p] * 4 + [c_int] * 5 + [c_void_p]),
     "cpi_hip_attention_prefill_window": (c_int, [c_void_p] * 4 + [c_int] * 6 + [c_void_p]),
     "cpi_hip_prefill_gemm": (c_int, [ctypes.POINTER(GemmDesc), c_void_p]),
+    "cpi_hip_prefill_gemm_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "cpi_hip_rmsnorm_rows_f32": (c_int, [c_void_p] * 3 + [c_int, c_int, c_float, c_void_p]),
     "cpi_hip_decode_fused_supported": (c_int, [c_void_p]),
     "cpi_hip_decode_step_fused": (c_int, [c_void_p, c_void_p]),

@@ -484,6 +484,11 @@ int cpi_hip_attention_prefill(const uint16_t* q, const uint16_t* k, const uint16
   return cpi_hip_attention_prefill_window(q, k, v, out, n, start, nh, nkv, hd, 0, s);
 }
 
+size_t cpi_hip_prefill_gemm_workspace_bytes(int out_features, int in_features, int num_tokens) {
+  if (out_features <= 0 || in_features < 64 || num_tokens <= 0) return 0;
+  return cpi::pgemm_workspace_bytes(out_features, in_features, num_tokens);
+}
+
 int cpi_hip_prefill_gemm(const cpi_gemm_desc* d, cpi_stream_t s) {
   if (!d) return fail("prefill_gemm: null descriptor");
   if (cpi::gemv_elems_per_chunk(d->wfmt) == 0) return fail("prefill_gemm: unknown weight format");
@@ -529,7 +534,9 @@ int cpi_hip_prefill_gemm(const cpi_gemm_desc* d, cpi_stream_t s) {
     p.v_cache = d->v_cache;
     p.max_ctx = d->max_context;
   }
-  return check(cpi::pgemm_launch(d->wfmt, p, S(s)), "prefill_gemm");
+  if (d->workspace && (reinterpret_cast<uintptr_t>(d->workspace) & 255) != 0)
+    return fail("prefill_gemm: workspace must be 256-byte aligned");
+  return check(cpi::pgemm_launch(d->wfmt, p, d->workspace, d->workspace_bytes, S(s)), "prefill_gemm");
 }
 
 int cpi_hip_decode_fused_supported(const cpi_fused_decode_desc* d) {

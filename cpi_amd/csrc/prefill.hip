@@ -16,6 +16,9 @@
 //   A operand: 8 fp16 of row c, B operand: 8 fp16 of column c, at k positions
 //   that are a function of (g, j) only, identical for A and B;
 //   D (4 fp32): rows 4 g + r (r = 0..3), column c.
+#include <algorithm>
+#include <cstdlib>
+
 #include "common.hpp"
 #include "../../include/cpi_hip.h"
 
@@ -48,10 +51,30 @@ __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(const float* x, const
 // ---------------------------------------------------------------------------
 // GEMM  Y[m, n] = sum_k X[m, k] W[n, k]  (W row-major [N, K] in a CPI_W_*
 // format, X fp16 [M, K]) with the engine's fused epilogues.
-// Tile: 64 weight rows x 64 tokens x 64 k per step, 4 waves, each wave 32 rows
-// x 32 tokens (2 x 2 MFMA blocks).  Weight and activation tiles are staged in
-// LDS (double buffered) with an 8-half row pad; global loads of step s+1 are
-// in flight while step s runs on the matrix cores.
+//
+// Workgroup tile: 128 weight rows x MT tokens (MT = 128 covers a whole
+// prefill chunk), k in steps of 128; 4 waves, each 32 rows x all MT tokens of
+// 16x16x32 MFMA blocks, so every dequantised weight operand feeds MT / 16
+// MFMAs.
+//   * Weights never touch LDS: each lane loads its rows' bytes straight into
+//     registers (k range 32 g .. 32 g + 31 of the step, g = lane / 16: 16 B of
+//     int4, 32 B of int8, 64 B of fp16) and expands them to fp16 MFMA A
+//     operands in place, one 8-k slice per MFMA sub-step.
+//   * Only the activation tile, which all four waves share, is staged in LDS:
+//     [MT tokens][16 chunks of 8 k], chunk q of token r stored at q ^ (r % 16)
+//     so the B-operand reads of 16 tokens hit distinct banks.  Two buffers;
+//     the next step's activations are loaded into registers during the MFMAs
+//     and written after them, the next-but-one step's weights likewise.
+//   * MFMA sub-step s uses, in lane g, k = 32 g + 8 s .. + 7 for both A and B,
+//     so the 4 sub-steps cover the 128 k of the step.
+// Per 128-k step a workgroup reads 4 * (MT * 256 B) of LDS for
+// 2 * 128 * MT * 128 flops (32 flop per LDS byte).
+//
+// Split-K: grid.y = ks slices of the k steps.  Each slice writes its fp32
+// tile to a partial buffer (device-coherent 16-byte stores), then bumps the
+// tile's arrival counter; the last slice to arrive sums all slices in slice
+// order (so the result does not depend on arrival order), resets the counter
+// and runs the epilogue.  ks = 1 needs no workspace.
 // ---------------------------------------------------------------------------
 struct PGemmParams {
   const uint8_t* w;
@@ -68,16 +91,26 @@ struct PGemmParams {
   uint16_t* k_cache;
   uint16_t* v_cache;
   int max_ctx;
+  // split-K
+  int ks, sps;          // slices, k steps per slice
+  float* part;          // [tiles][ks][rows * MT] partial tiles, thread-major
+  uint32_t* counters;   // [tiles] arrival counters, zero between launches
 };
 
-constexpr int kPT = 64;        // tile rows / tokens / k
-constexpr int kPLd = kPT + 8;  // LDS row stride in halves (bank spread)
+constexpr int kPK = 128;                // k per step
+constexpr int kPCounters = 4096;        // arrival counters at the head of the workspace
+constexpr size_t kPCounterBytes = kPCounters * sizeof(uint32_t);
+static_assert(kPCounterBytes == CPI_PREFILL_COUNTER_BYTES, "counter area of the C-ABI");
+constexpr int kPTargetWgs = 512;        // split-K target workgroups at 64-row tiles
+constexpr int kPSplit128 = 4;           // k slices at 128-row tiles
+constexpr int kPMaxSplit = 8;
+constexpr int kPMinSteps = 2;           // k steps per slice at least
 
-// Weight bytes of 16 consecutive k values of one row.
+// Weight registers of one lane for one step: 32 k of one row.
 template <int FMT> struct PW;
-template <> struct PW<CPI_W_F16> { typedef u32x4 T[2]; static constexpr int kBytes = 32; };
-template <> struct PW<CPI_W_I8ROW> { typedef u32x4 T[1]; static constexpr int kBytes = 16; };
-template <> struct PW<CPI_W_I4ROW> { typedef uint2 T[1]; static constexpr int kBytes = 8; };
+template <> struct PW<CPI_W_F16> { static constexpr int kVec = 4; };    // 64 B
+template <> struct PW<CPI_W_I8ROW> { static constexpr int kVec = 2; };  // 32 B
+template <> struct PW<CPI_W_I4ROW> { static constexpr int kVec = 1; };  // 16 B
 template <> struct PW<CPI_W_I4G32> : PW<CPI_W_I4ROW> {};
 
 // Offset-binary bytes (b' = q + 128) or nibbles (n' = q + 8) sit under the
@@ -86,199 +119,335 @@ __device__ __forceinline__ uint32_t pair_bits(uint32_t hi_src, uint32_t lo_src, 
   return __builtin_amdgcn_perm(hi_src, lo_src, sel) | 0x64006400u;
 }
 
-// 16 fp16 weights (q, or q * group scale for I4G32) in natural k order.
+// fp16 A operand of sub-step s (8 consecutive k) from a lane's 32-k registers:
+// q, q * group scale for I4G32, the fp16 weights themselves for F16.
 template <int FMT>
-__device__ __forceinline__ void dequant16(const typename PW<FMT>::T& raw, uint16_t gscale, uint32_t* out) {
+__device__ __forceinline__ h8 dequant8(const u32x4* raw, int s, f16x2 sc) {
+  u32x4 out;
   if constexpr (FMT == CPI_W_F16) {
-    out[0] = raw[0].x; out[1] = raw[0].y; out[2] = raw[0].z; out[3] = raw[0].w;
-    out[4] = raw[1].x; out[5] = raw[1].y; out[6] = raw[1].z; out[7] = raw[1].w;
+    out = raw[s];
   } else if constexpr (FMT == CPI_W_I8ROW) {
-    const uint32_t d[4] = {raw[0].x, raw[0].y, raw[0].z, raw[0].w};
+    const u32x4 r = raw[s >> 1];
+    const uint32_t d0 = ((s & 1) ? r.z : r.x) ^ 0x80808080u;
+    const uint32_t d1 = ((s & 1) ? r.w : r.y) ^ 0x80808080u;
     const f16x2 bias = {static_cast<f16>(-1152.f), static_cast<f16>(-1152.f)};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t v = d[i] ^ 0x80808080u;
-      const f16x2 a = as_h2(pair_bits(0u, v, 0x0c010c00u)) + bias;
-      const f16x2 b = as_h2(pair_bits(0u, v, 0x0c030c02u)) + bias;
-      out[2 * i] = __builtin_bit_cast(uint32_t, a);
-      out[2 * i + 1] = __builtin_bit_cast(uint32_t, b);
-    }
+    out.x = __builtin_bit_cast(uint32_t, as_h2(pair_bits(0u, d0, 0x0c010c00u)) + bias);
+    out.y = __builtin_bit_cast(uint32_t, as_h2(pair_bits(0u, d0, 0x0c030c02u)) + bias);
+    out.z = __builtin_bit_cast(uint32_t, as_h2(pair_bits(0u, d1, 0x0c010c00u)) + bias);
+    out.w = __builtin_bit_cast(uint32_t, as_h2(pair_bits(0u, d1, 0x0c030c02u)) + bias);
   } else {
-    const uint32_t d[2] = {raw[0].x, raw[0].y};
+    const u32x4 r = raw[0];
+    const uint32_t word = s == 0 ? r.x : (s == 1 ? r.y : (s == 2 ? r.z : r.w));
+    const uint32_t v = word ^ 0x88888888u;
+    const uint32_t lo = v & 0x0F0F0F0Fu;         // even k of each byte
+    const uint32_t hi = (v >> 4) & 0x0F0F0F0Fu;  // odd k
     const f16x2 bias = {static_cast<f16>(-1032.f), static_cast<f16>(-1032.f)};
-    f16x2 sc;
-    if constexpr (FMT == CPI_W_I4G32) {
-      sc.x = __builtin_bit_cast(f16, gscale);
-      sc.y = sc.x;
-    }
+    uint32_t o[4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t v = d[i] ^ 0x88888888u;
-      const uint32_t lo = v & 0x0F0F0F0Fu;         // even k of each byte
-      const uint32_t hi = (v >> 4) & 0x0F0F0F0Fu;  // odd k
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t sel = 0x0c000c00u | (static_cast<uint32_t>(b + 4) << 16) | static_cast<uint32_t>(b);
-        f16x2 q = as_h2(pair_bits(hi, lo, sel)) + bias;
-        if constexpr (FMT == CPI_W_I4G32) q = q * sc;
-        out[4 * i + b] = __builtin_bit_cast(uint32_t, q);
-      }
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t sel = 0x0c000c00u | (static_cast<uint32_t>(b + 4) << 16) | static_cast<uint32_t>(b);
+      f16x2 q = as_h2(pair_bits(hi, lo, sel)) + bias;
+      if constexpr (FMT == CPI_W_I4G32) q = q * sc;
+      o[b] = __builtin_bit_cast(uint32_t, q);
     }
+    out = u32x4{o[0], o[1], o[2], o[3]};
   }
+  return __builtin_bit_cast(h8, out);
 }
 
 __device__ __forceinline__ float silu(float g) { return g / (1.f + expf(-g)); }
 
-template <int FMT>
+// Device-coherent 16-byte accesses (agent scope, sc1) for the split-K
+// partials, through a raw buffer descriptor over [base, base + 2 GiB).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coh_rsrc(const float* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, 0x7fffffff, 0x00020000);
+}
+constexpr int kCohAux = 16;  // sc1
+
+// One element of the fused epilogues: (nl, ml) of the fp32 tile in LDS
+// (rows nl of stride ld), global row n0 + nl and token m.
+__device__ __forceinline__ void pgemm_epilogue(const PGemmParams& p, const float* Cs, int ld, int n0, int nl,
+                                               int ml, int m, const float* rsc) {
+  const int n = n0 + nl;
+  auto val = [&](int nll) {
+    float v = Cs[nll * ld + ml];
+    if (rsc) v *= p.scale_count == 1 ? rsc[0] : rsc[n0 + nll];
+    return v;
+  };
+  const float v = val(nl);
+  switch (p.epi) {
+    case CPI_EPI_STORE_F32: static_cast<float*>(p.y)[static_cast<size_t>(m) * p.N + n] = v; break;
+    case CPI_EPI_STORE_F16: static_cast<uint16_t*>(p.y)[static_cast<size_t>(m) * p.N + n] = f2h(v); break;
+    case CPI_EPI_RESID_ADD: static_cast<float*>(p.y)[static_cast<size_t>(m) * p.N + n] += v; break;
+    case CPI_EPI_SWIGLU: {
+      // tile of 8 rows: w1 rows 4T..4T+3, then the matching w3 rows
+      const int r = n & 7;
+      if (r < 4) {
+        const float u = val(nl + 4);
+        static_cast<uint16_t*>(p.y)[static_cast<size_t>(m) * (p.N / 2) + (n >> 3) * 4 + r] = f2h(silu(v) * u);
+      }
+      break;
+    }
+    case CPI_EPI_QKV_ROPE: {
+      const int T = n >> 3, r = n & 7;
+      const int hd = p.hd, half = hd >> 1, tph = hd / 8;
+      const int q_tiles = p.nh * tph, k_tiles = p.nkv * tph;
+      const int kvdim = p.nkv * hd;
+      const int pos = p.start + m;
+      if (T < q_tiles + k_tiles) {
+        const bool is_q = T < q_tiles;
+        const int u = is_q ? T : T - q_tiles;
+        const int head = u / tph;
+        const int dd = 4 * (u % tph) + (r & 3);
+        const float other = val(nl ^ 4);
+        const float cs = p.rope_cos[static_cast<size_t>(pos) * half + dd];
+        const float sn = p.rope_sin[static_cast<size_t>(pos) * half + dd];
+        float outv;
+        int d;
+        if (r < 4) {
+          outv = v * cs - other * sn;
+          d = dd;
+        } else {
+          outv = other * sn + v * cs;
+          d = dd + half;
+        }
+        if (is_q)
+          static_cast<uint16_t*>(p.y)[static_cast<size_t>(m) * p.nh * hd + head * hd + d] = f2h(outv);
+        else if (pos < p.max_ctx)
+          p.k_cache[static_cast<size_t>(pos) * kvdim + head * hd + d] = f2h(outv);
+      } else {
+        const int vr = (T - q_tiles - k_tiles) * 8 + r;
+        if (pos < p.max_ctx && vr < kvdim) p.v_cache[static_cast<size_t>(pos) * kvdim + vr] = f2h(v);
+      }
+      break;
+    }
+  }
+}
+
+template <int FMT, int MT, int RB>
 __global__ void __launch_bounds__(256) pgemm_kernel(PGemmParams p) {
-  __shared__ __align__(16) uint16_t Ws[2][kPT * kPLd];
-  __shared__ __align__(16) uint16_t Xs[2][kPT * kPLd];
-  __shared__ float Cs[kPT][kPT + 1];
+  constexpr int kPR = 64 * RB;                     // weight rows per tile (RB 16-row blocks per wave)
+  constexpr int NB = MT / 16;                      // 16-token blocks per wave (all tokens)
+  constexpr int XV = MT / 16;                      // 16-byte activation loads per thread and step
+  constexpr int kXsBytes = MT * kPK * 2;           // one activation buffer
+  constexpr int kCsLd = MT / 2 + 1;                // epilogue half-tile stride (floats)
+  static_assert(kPR * kCsLd * 4 <= 2 * kXsBytes, "epilogue tile fits in the activation buffers");
+  constexpr int WV = PW<FMT>::kVec;
+  __shared__ __align__(16) uint8_t smem[2 * kXsBytes];
 
   const int t = threadIdx.x;
   const int lane = t & 63;
   const int wave = t >> 6;
   const int g = lane >> 4, c = lane & 15;
-  const int n0 = blockIdx.x * kPT;
-  const int m0 = blockIdx.y * kPT;
+  const int tile = blockIdx.x;
+  const int slice = blockIdx.y;
+  const int n0 = tile * kPR;
+  const int m0 = blockIdx.z * MT;
   const int K = p.K;
+  const int nk = (K + kPK - 1) / kPK;
+  const int kb = slice * p.sps;
+  const int nsteps = min(kb + p.sps, nk) - kb;
+  const int wr0 = 16 * RB * wave;
 
-  // loader role: row / token t/4, 16 k values at 16*(t%4)
-  const int lr = t >> 2, lq = t & 3;
-  const int wrow = min(n0 + lr, p.N - 1);
-  const int xtok = min(m0 + lr, p.M - 1);
-  const size_t row_bytes = FMT == CPI_W_F16 ? 2u * K : (FMT == CPI_W_I8ROW ? static_cast<size_t>(K) : K / 2u);
-  const uint8_t* wsrc = p.w + static_cast<size_t>(wrow) * row_bytes + lq * PW<FMT>::kBytes;
-  const uint16_t* xsrc = p.x + static_cast<size_t>(xtok) * K + 16 * lq;
-  const uint16_t* gsrc = FMT == CPI_W_I4G32
-                             ? static_cast<const uint16_t*>(p.scales) + static_cast<size_t>(wrow) * (K / 32) + lq / 2
-                             : nullptr;
-
-  typename PW<FMT>::T wr;
-  u32x4 xr[2];
-  uint16_t gs = 0;
-  auto load = [&](int kt) {
-    const uint8_t* ws = wsrc + static_cast<size_t>(kt) * (PW<FMT>::kBytes * 4);
-    if constexpr (FMT == CPI_W_F16) {
-      wr[0] = *reinterpret_cast<const u32x4*>(ws);
-      wr[1] = *reinterpret_cast<const u32x4*>(ws + 16);
-    } else if constexpr (FMT == CPI_W_I8ROW) {
-      wr[0] = *reinterpret_cast<const u32x4*>(ws);
-    } else {
-      wr[0] = *reinterpret_cast<const uint2*>(ws);
+  // All operand loads are raw buffer loads: one 32-bit lane offset each, the
+  // row-block / vector / step offsets in scalar registers, and the
+  // descriptor's range check returns zeros past the last weight row / token.
+  // ---- weights: rows n0 + wr0 + 16 i + c, bytes of k = 32 g .. 32 g + 31 of a step
+  const uint32_t row_bytes = FMT == CPI_W_F16 ? 2u * K : (FMT == CPI_W_I8ROW ? static_cast<uint32_t>(K) : K / 2u);
+  constexpr int kStepBytes = WV * 16 * 4;          // bytes of one row per 128-k step
+  const int rows_left = p.N - n0;
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint8_t*>(p.w) + static_cast<size_t>(n0) * row_bytes, 0, rows_left * row_bytes, 0x00020000);
+  const uint32_t wvoff = (wr0 + c) * row_bytes + g * (WV * 16);
+  const uint32_t gstride = static_cast<uint32_t>(K / 32) * 2u;   // scale bytes per row
+  __amdgpu_buffer_rsrc_t grs = wrs;
+  if constexpr (FMT == CPI_W_I4G32)
+    grs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(static_cast<const uint8_t*>(p.scales)) + static_cast<size_t>(n0) * gstride, 0,
+        rows_left * gstride, 0x00020000);
+  const uint32_t gvoff = (wr0 + c) * gstride + 2u * g;
+  struct WRegs {
+    u32x4 w[RB][WV];
+    f16x2 sc[RB];
+  };
+  // k beyond K (a final half step when K % 128 == 64) reads finite bytes of
+  // the next row (or zeros) that meet zeroed activations
+  auto load_w = [&](WRegs& r, int kt) {
+#pragma unroll
+    for (int i = 0; i < RB; ++i) {
+#pragma unroll
+      for (int v = 0; v < WV; ++v)
+        r.w[i][v] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvoff, 16 * i * row_bytes + kt * kStepBytes + 16 * v, 0);
+      if constexpr (FMT == CPI_W_I4G32) {
+        const f16 s = __builtin_bit_cast(
+            f16, __builtin_amdgcn_raw_buffer_load_b16(grs, gvoff, 16 * i * gstride + kt * 8, 0));
+        r.sc[i] = f16x2{s, s};
+      }
     }
-    if constexpr (FMT == CPI_W_I4G32) gs = gsrc[kt * 2];
-    const uint16_t* xs = xsrc + static_cast<size_t>(kt) * kPT;
-    xr[0] = *reinterpret_cast<const u32x4*>(xs);
-    xr[1] = *reinterpret_cast<const u32x4*>(xs + 8);
-  };
-  auto stage = [&](int buf) {
-    uint32_t d[8];
-    dequant16<FMT>(wr, gs, d);
-    u32x4* wdst = reinterpret_cast<u32x4*>(&Ws[buf][lr * kPLd + 16 * lq]);
-    wdst[0] = u32x4{d[0], d[1], d[2], d[3]};
-    wdst[1] = u32x4{d[4], d[5], d[6], d[7]};
-    u32x4* xdst = reinterpret_cast<u32x4*>(&Xs[buf][lr * kPLd + 16 * lq]);
-    xdst[0] = xr[0];
-    xdst[1] = xr[1];
   };
 
-  // wave tile: rows 32*(wave/2), tokens 32*(wave%2)
-  const int wr0 = 32 * (wave >> 1), wt0 = 32 * (wave & 1);
-  f4 acc[2][2];
+  // ---- activations: chunk L = v * 256 + t -> token L / 16, chunk L % 16
+  // (L % 16 == t % 16 for every v)
+  const int toks_left = p.M - m0;
+  const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(p.x) + static_cast<size_t>(m0) * K, 0, toks_left * K * 2, 0x00020000);
+  const uint32_t xvoff = (t >> 4) * (2u * K) + 16u * (t & 15);
+  u32x4 xr[XV];
+  auto load_x = [&](int kt) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int v = 0; v < XV; ++v) xr[v] = __builtin_amdgcn_raw_buffer_load_b128(xrs, xvoff, v * 32 * K + kt * 256, 0);
+  };
+  auto store_x = [&](int buf, int kt) {
+    const bool ok = kt * kPK + 8 * (t & 15) < K;
+    uint8_t* xs = smem + buf * kXsBytes;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int v = 0; v < XV; ++v) {
+      const int L = v * 256 + t;
+      const int r = L >> 4, q = L & 15;
+      *reinterpret_cast<u32x4*>(xs + r * 256 + 16 * (q ^ (r & 15))) = ok ? xr[v] : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
 
-  const int nk = K / kPT;
-  load(0);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int buf = kt & 1;
-    stage(buf);
-    __syncthreads();
-    if (kt + 1 < nk) load(kt + 1);
+  f4 acc[RB][NB];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      h8 a[2], b[2];
+  for (int i = 0; i < RB; ++i)
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        a[i] = *reinterpret_cast<const h8*>(&Ws[buf][(wr0 + 16 * i + c) * kPLd + 32 * s + 8 * g]);
-        b[i] = *reinterpret_cast<const h8*>(&Xs[buf][(wt0 + 16 * i + c) * kPLd + 32 * s + 8 * g]);
+    for (int j = 0; j < NB; ++j) acc[i][j] = f4{0.f, 0.f, 0.f, 0.f};
+
+  // Sub-step s + 1's operands (LDS reads, dequantisation) are requested
+  // before sub-step s's MFMAs, so their latency hides behind the matrix work.
+  auto mma = [&](int buf, const WRegs& W) {
+    const uint8_t* xs = smem + buf * kXsBytes;
+    auto read_b = [&](h8* b, int s) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j) {
+        const int r = 16 * j + c;
+        b[j] = *reinterpret_cast<const h8*>(xs + r * 256 + 16 * ((4 * g + s) ^ (r & 15)));
+      }
+    };
+    h8 b0[NB], b1[NB], a0[RB], a1[RB];
+    read_b(b0, 0);
+#pragma unroll
+    for (int i = 0; i < RB; ++i) a0[i] = dequant8<FMT>(W.w[i], 0, W.sc[i]);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      h8* bc = (s & 1) ? b1 : b0;
+      h8* bn = (s & 1) ? b0 : b1;
+      h8* ac = (s & 1) ? a1 : a0;
+      h8* an = (s & 1) ? a0 : a1;
+      if (s < 3) {
+        read_b(bn, s + 1);
+#pragma unroll
+        for (int i = 0; i < RB; ++i) an[i] = dequant8<FMT>(W.w[i], s + 1, W.sc[i]);
       }
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < RB; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma16(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < NB; ++j) acc[i][j] = mfma16(ac[i], bc[j], acc[i][j]);
+    }
+  };
+
+  // Step j computes from LDS buffer j % 2 and weight set j % 2.  During it the
+  // activations of step j + 1 are in flight (written to the other buffer
+  // after the MFMAs) and, once the MFMAs have consumed the weight set, the
+  // weights of step j + 2 are requested into it.  The barrier at the top of
+  // step j publishes buffer j % 2 and frees buffer (j + 1) % 2, whose last
+  // reader was step j - 1.  Loads are issued unconditionally (steps past the
+  // slice re-read its last step, unused), so the number of loads in flight is
+  // the same on every path and the waits stay partial.
+  const int klast = kb + max(nsteps, 1) - 1;
+  auto cl = [&](int kt) { return kt < klast ? kt : klast; };
+  WRegs w0, w1;
+  load_x(kb);
+  load_w(w0, kb);
+  load_w(w1, cl(kb + 1));
+  store_x(0, kb);
+  for (int j = 0; j < nsteps; j += 2) {
+    lds_barrier();
+    load_x(cl(kb + j + 1));
+    mma(0, w0);
+    load_w(w0, cl(kb + j + 2));
+    store_x(1, kb + j + 1);
+    lds_barrier();
+    load_x(cl(kb + j + 2));
+    if (j + 1 < nsteps) mma(1, w1);
+    load_w(w1, cl(kb + j + 3));
+    store_x(0, kb + j + 2);
+  }
+
+  // ---- split-K: publish this slice, the last arrival reduces in slice order
+  int* flag = reinterpret_cast<int*>(smem);  // the buffers are free once every wave is past its MFMAs
+  if (p.ks > 1) {
+    constexpr int NV = RB * NB;  // 16-byte partial vectors per thread
+    const size_t tid_lin = static_cast<size_t>(blockIdx.z) * gridDim.x + tile;
+    const float* part = p.part + tid_lin * p.ks * (256 * NV * 4);
+    const __amdgpu_buffer_rsrc_t rs = coh_rsrc(part);
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[i][j]), rs,
+                                               ((slice * NV + i * NB + j) * 256 + t) * 16, 0, kCohAux);
+    // the partial stores are device-coherent (write-through); their completion
+    // orders them before the counter update without an L2 writeback
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    uint32_t* cnt = p.counters + tid_lin;
+    if (t == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *flag = prev == static_cast<uint32_t>(p.ks - 1);
+    }
+    __syncthreads();
+    const bool last = *flag != 0;
+    __syncthreads();  // the flag word is overwritten by the epilogue tile
+    if (!last) return;
+    if (t == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // every slice, this one included, is read back from the partial buffer
+    // two slices per round (32 KB+ per round in flight per workgroup), and
+    // added in slice order
+    auto ld = [&](f4 (&v)[NB], int s, int i) {
+#pragma unroll
+      for (int j = 0; j < NB; ++j)
+        v[j] = __builtin_bit_cast(
+            f4, __builtin_amdgcn_raw_buffer_load_b128(rs, ((s * NV + i * NB + j) * 256 + t) * 16, 0, kCohAux));
+    };
+    for (int s = 0; s < p.ks; s += 2) {
+#pragma unroll
+      for (int i = 0; i < RB; ++i) {
+        f4 v0[NB], v1[NB];
+        ld(v0, s, i);
+        if (s + 1 < p.ks) ld(v1, s + 1, i);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[i][j] = s == 0 ? v0[j] : acc[i][j] + v0[j];
+        if (s + 1 < p.ks) {
+#pragma unroll
+          for (int j = 0; j < NB; ++j) acc[i][j] += v1[j];
+        }
+      }
     }
   }
 
-  // D rows are weight rows (n), columns tokens (m)
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) Cs[wr0 + 16 * i + 4 * g + r][wt0 + 16 * j + c] = acc[i][j][r];
-  __syncthreads();
-
+  // ---- epilogue, one token half at a time: every wave stages its D blocks of
+  // that half (rows 16 i + 4 (lane / 16) + r, token 16 j + lane % 16) in LDS
+  // over the activation buffers, then every thread applies the epilogue
   const float* rsc = (FMT == CPI_W_I8ROW || FMT == CPI_W_I4ROW) ? static_cast<const float*>(p.scales) : nullptr;
-  for (int e = t; e < kPT * kPT; e += 256) {
-    const int nl = e & (kPT - 1), ml = e / kPT;
-    const int n = n0 + nl, m = m0 + ml;
-    if (n >= p.N || m >= p.M) continue;
-    auto val = [&](int nll) {
-      float v = Cs[nll][ml];
-      if (rsc) v *= p.scale_count == 1 ? rsc[0] : rsc[n0 + nll];
-      return v;
-    };
-    const float v = val(nl);
-    switch (p.epi) {
-      case CPI_EPI_STORE_F32: static_cast<float*>(p.y)[static_cast<size_t>(m) * p.N + n] = v; break;
-      case CPI_EPI_STORE_F16: static_cast<uint16_t*>(p.y)[static_cast<size_t>(m) * p.N + n] = f2h(v); break;
-      case CPI_EPI_RESID_ADD: static_cast<float*>(p.y)[static_cast<size_t>(m) * p.N + n] += v; break;
-      case CPI_EPI_SWIGLU: {
-        // tile of 8 rows: w1 rows 4T..4T+3, then the matching w3 rows
-        const int r = n & 7;
-        if (r < 4) {
-          const float u = val(nl + 4);
-          static_cast<uint16_t*>(p.y)[static_cast<size_t>(m) * (p.N / 2) + (n >> 3) * 4 + r] = f2h(silu(v) * u);
-        }
-        break;
-      }
-      case CPI_EPI_QKV_ROPE: {
-        const int T = n >> 3, r = n & 7;
-        const int hd = p.hd, half = hd >> 1, tph = hd / 8;
-        const int q_tiles = p.nh * tph, k_tiles = p.nkv * tph;
-        const int kvdim = p.nkv * hd;
-        const int pos = p.start + m;
-        if (T < q_tiles + k_tiles) {
-          const bool is_q = T < q_tiles;
-          const int u = is_q ? T : T - q_tiles;
-          const int head = u / tph;
-          const int dd = 4 * (u % tph) + (r & 3);
-          const float other = val(nl ^ 4);
-          const float cs = p.rope_cos[static_cast<size_t>(pos) * half + dd];
-          const float sn = p.rope_sin[static_cast<size_t>(pos) * half + dd];
-          float outv;
-          int d;
-          if (r < 4) {
-            outv = v * cs - other * sn;
-            d = dd;
-          } else {
-            outv = other * sn + v * cs;
-            d = dd + half;
-          }
-          if (is_q)
-            static_cast<uint16_t*>(p.y)[static_cast<size_t>(m) * p.nh * hd + head * hd + d] = f2h(outv);
-          else if (pos < p.max_ctx)
-            p.k_cache[static_cast<size_t>(pos) * kvdim + head * hd + d] = f2h(outv);
-        } else {
-          const int vr = (T - q_tiles - k_tiles) * 8 + r;
-          if (pos < p.max_ctx && vr < kvdim) p.v_cache[static_cast<size_t>(pos) * kvdim + vr] = f2h(v);
-        }
-        break;
-      }
+  float* Cs = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < RB; ++i)
+#pragma unroll
+      for (int j = 0; j < NB / 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          Cs[(wr0 + 16 * i + 4 * g + r) * kCsLd + 16 * j + c] = acc[i][(NB / 2) * h + j][r];
+    lds_barrier();
+    for (int e = t; e < kPR * (MT / 2); e += 256) {
+      const int nl = e & (kPR - 1), ml = e / kPR;
+      const int m = m0 + (MT / 2) * h + ml;
+      if (n0 + nl >= p.N || m >= p.M) continue;
+      pgemm_epilogue(p, Cs, kCsLd, n0, nl, ml, m, rsc);
     }
   }
 }
@@ -438,16 +607,80 @@ hipError_t rmsnorm_rows_launch(const float* x, const uint16_t* w, uint16_t* y, i
   return hipGetLastError();
 }
 
-hipError_t pgemm_launch(int wfmt, const PGemmParams& p, hipStream_t s) {
-  const dim3 grid((p.N + kPT - 1) / kPT, (p.M + kPT - 1) / kPT);
+// Launch shape of the prefill GEMM: token tile, k slices and the workspace
+// those slices need (counters, then partial tiles).
+struct PGemmPlan {
+  int rb, rows, mt, tiles, ttiles, nk, ks, sps;
+  size_t workspace;
+};
+
+// Optional integer override of a plan choice from the environment (tuning).
+inline int pgemm_env(const char* name) {
+  const char* v = std::getenv(name);
+  return v ? std::atoi(v) : 0;
+}
+
+// Row tile 128 (two 16-row blocks per wave) for wide outputs, 64 otherwise, so
+// narrow outputs (o_proj, w2) start more workgroups before splitting k; then
+// k slices: 4 at 128-row tiles, enough for kPTargetWgs workgroups at 64 rows
+// (measured on MI355X at
+// chunk 128: qkv and w1|w3 fastest at 128 rows and 3-4 slices, o_proj and w2
+// at 64 rows and 8 slices).
+inline PGemmPlan pgemm_plan(int N, int K, int M, size_t workspace_avail) {
+  static const int force_rows = pgemm_env("CPI_PREFILL_TILE_ROWS");
+  static const int force_split = pgemm_env("CPI_PREFILL_SPLIT");
+  PGemmPlan pl;
+  pl.rb = (force_rows == 64 || (force_rows != 128 && N < 8192)) ? 1 : 2;
+  pl.rows = 64 * pl.rb;
+  pl.mt = M > 64 ? 128 : 64;
+  pl.tiles = (N + pl.rows - 1) / pl.rows;
+  pl.ttiles = (M + pl.mt - 1) / pl.mt;
+  pl.nk = (K + kPK - 1) / kPK;
+  const int base = pl.tiles * pl.ttiles;
+  int ks = force_split > 0 ? force_split : (pl.rb == 2 ? kPSplit128 : (kPTargetWgs + base - 1) / base);
+  ks = std::min(ks, std::min(kPMaxSplit, std::max(1, pl.nk / kPMinSteps)));
+  if (base > kPCounters) ks = 1;
+  auto bytes = [&](int k) {
+    return k > 1 ? kPCounterBytes + static_cast<size_t>(base) * k * pl.rows * pl.mt * sizeof(float) : size_t{0};
+  };
+  while (ks > 1 && bytes(ks) > workspace_avail) --ks;
+  pl.sps = (pl.nk + ks - 1) / ks;
+  pl.ks = (pl.nk + pl.sps - 1) / pl.sps;  // no empty slice
+  pl.workspace = bytes(pl.ks);
+  return pl;
+}
+
+// Workspace bytes for the split-K shape of (N, K, M) with unlimited space.
+inline size_t pgemm_workspace_bytes(int N, int K, int M) {
+  return pgemm_plan(N, K, M, ~size_t{0}).workspace;
+}
+
+template <int FMT>
+hipError_t pgemm_launch_fmt(const PGemmParams& p, const PGemmPlan& pl, dim3 grid, hipStream_t s) {
+  if (pl.mt == 128 && pl.rb == 2) hipLaunchKernelGGL((pgemm_kernel<FMT, 128, 2>), grid, dim3(256), 0, s, p);
+  else if (pl.mt == 128) hipLaunchKernelGGL((pgemm_kernel<FMT, 128, 1>), grid, dim3(256), 0, s, p);
+  else if (pl.rb == 2) hipLaunchKernelGGL((pgemm_kernel<FMT, 64, 2>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((pgemm_kernel<FMT, 64, 1>), grid, dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+// `workspace` (may be null) must hold zeroed counters in its first
+// kPCounterBytes before the first call; every call leaves them zero.  Calls
+// that share a workspace must not overlap.
+hipError_t pgemm_launch(int wfmt, PGemmParams p, void* workspace, size_t workspace_bytes, hipStream_t s) {
+  const PGemmPlan pl = pgemm_plan(p.N, p.K, p.M, workspace ? workspace_bytes : 0);
+  p.ks = pl.ks;
+  p.sps = pl.sps;
+  p.counters = static_cast<uint32_t*>(workspace);
+  p.part = workspace ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + kPCounterBytes) : nullptr;
+  const dim3 grid(pl.tiles, pl.ks, pl.ttiles);
   switch (wfmt) {
-    case CPI_W_F16: hipLaunchKernelGGL(pgemm_kernel<CPI_W_F16>, grid, dim3(256), 0, s, p); break;
-    case CPI_W_I8ROW: hipLaunchKernelGGL(pgemm_kernel<CPI_W_I8ROW>, grid, dim3(256), 0, s, p); break;
-    case CPI_W_I4ROW: hipLaunchKernelGGL(pgemm_kernel<CPI_W_I4ROW>, grid, dim3(256), 0, s, p); break;
-    case CPI_W_I4G32: hipLaunchKernelGGL(pgemm_kernel<CPI_W_I4G32>, grid, dim3(256), 0, s, p); break;
+    case CPI_W_F16: return pgemm_launch_fmt<CPI_W_F16>(p, pl, grid, s);
+    case CPI_W_I8ROW: return pgemm_launch_fmt<CPI_W_I8ROW>(p, pl, grid, s);
+    case CPI_W_I4ROW: return pgemm_launch_fmt<CPI_W_I4ROW>(p, pl, grid, s);
+    case CPI_W_I4G32: return pgemm_launch_fmt<CPI_W_I4G32>(p, pl, grid, s);
     default: return hipErrorInvalidValue;
   }
-  return hipGetLastError();
 }
 
 hipError_t attn_prefill_launch(const APParams& p, int hd, hipStream_t s) {

@@ -390,6 +390,18 @@ void LlamaEngine::initialize(const EngineOptions& options) {
       pq_ = static_cast<uint16_t*>(dmalloc(C * q_dim_ * 2));
       patt_ = static_cast<uint16_t*>(dmalloc(C * q_dim_ * 2));
       pff_ = static_cast<uint16_t*>(dmalloc(C * I * 2));
+      // split-K workspace of the prefill GEMMs: large enough for every
+      // projection at a full chunk and at a short (<= 64-token) tail chunk
+      for (const int m : {prefill_chunk_, std::min(prefill_chunk_, 64)}) {
+        pws_bytes_ = std::max({pws_bytes_, cpi_hip_prefill_gemm_workspace_bytes(q_dim_ + 2 * kv_dim_, H, m),
+                               cpi_hip_prefill_gemm_workspace_bytes(H, q_dim_, m),
+                               cpi_hip_prefill_gemm_workspace_bytes(2 * I, H, m),
+                               cpi_hip_prefill_gemm_workspace_bytes(H, I, m)});
+      }
+      if (pws_bytes_ > 0) {
+        pws_ = dmalloc(pws_bytes_);
+        HIP_OK(hipMemset(pws_, 0, CPI_PREFILL_COUNTER_BYTES));  // arrival counters start at zero
+      }
     }
   }
   HIP_OK(hipDeviceSynchronize());
@@ -573,6 +585,7 @@ void LlamaEngine::prefill_chunked(const std::vector<int>& prompt, int n_pre) {
     d.wfmt = L.wfmt; d.w = L.w; d.scales = L.scales; d.scale_count = L.scale_count;
     d.out_features = L.rows; d.in_features = L.cols; d.x = x; d.num_tokens = rows;
     d.epilogue = epi; d.y = y;
+    d.workspace = pws_; d.workspace_bytes = pws_bytes_;
     return d;
   };
   for (int c0 = 0; c0 < n_pre; c0 += prefill_chunk_) {

@@ -209,6 +209,8 @@ class LlamaEngine {
   int prefill_chunk_ = 1;
   float* px_ = nullptr;
   uint16_t *pxn_ = nullptr, *pq_ = nullptr, *patt_ = nullptr, *pff_ = nullptr;
+  void* pws_ = nullptr;  // prefill GEMM split-K workspace
+  std::size_t pws_bytes_ = 0;
 
   float* capture_ = nullptr;
   int capture_steps_ = 0;

@@ -98,7 +98,8 @@ def time_gemv(fmt: str, R: int, K: int, rotate_bytes: int = 3 << 30, iters: int 
 PEAK_F16_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
 
 
-def time_prefill_gemm(fmt: str, N: int, K: int, M: int = 128, iters: int = 50, rotate_bytes: int = 1 << 30):
+def time_prefill_gemm(fmt: str, N: int, K: int, M: int = 128, iters: int = 50, rotate_bytes: int = 1 << 30,
+                      split: bool = True):
     """Kernel-only chunked-prefill GEMM: M tokens x (N x K) weights, plain fp32
     store.  Returns dict(us, tflops, mfma_frac)."""
     gen = torch.Generator(device="cuda").manual_seed(N + K + M)
@@ -107,12 +108,16 @@ def time_prefill_gemm(fmt: str, N: int, K: int, M: int = 128, iters: int = 50, r
     bufs = [_weights(fmt, N, K, gen) for _ in range(copies)]
     x = torch.randn(M * K, device="cuda", generator=gen).half()
     y = torch.empty(M * N, device="cuda", dtype=torch.float32)
+    ws_bytes = _lib.lib().cpi_hip_prefill_gemm_workspace_bytes(N, K, M) if split else 0
+    ws = torch.zeros(max(ws_bytes, 1), device="cuda", dtype=torch.uint8)
     descs = []
     for w, s, sc in bufs:
         d = _lib.GemmDesc()
         d.wfmt, d.w, d.scales, d.scale_count = FMT_CODE[fmt], w.data_ptr(), (s.data_ptr() if s is not None else 0), sc
         d.out_features, d.in_features, d.x, d.num_tokens = N, K, x.data_ptr(), M
         d.epilogue, d.y = _lib.EPI_STORE_F32, y.data_ptr()
+        if ws_bytes:
+            d.workspace, d.workspace_bytes = ws.data_ptr(), ws_bytes
         descs.append(d)
     fn = _lib.lib().cpi_hip_prefill_gemm
 
@@ -139,7 +144,7 @@ def time_prefill_gemm(fmt: str, N: int, K: int, M: int = 128, iters: int = 50, r
     tflops = 2.0 * M * N * K / us / 1e6
     del g, bufs
     torch.cuda.empty_cache()
-    return {"fmt": fmt, "N": N, "K": K, "M": M, "us": us, "tflops": tflops, "mfma_frac": tflops / PEAK_F16_TFLOPS,
+    return {"fmt": fmt, "N": N, "K": K, "M": M, "split": split, "us": us, "tflops": tflops, "mfma_frac": tflops / PEAK_F16_TFLOPS,
             "weight_gbps": wbytes / us / 1e3}
 
 
@@ -223,9 +228,10 @@ if __name__ == "__main__":
     if sys.argv[1:2] == ["prefill"]:
         for f in ("i4g32", "f16"):
             for name, R, K in GEMV_SHAPES:
-                r = time_prefill_gemm(f, R, K)
-                r["shape"] = name
-                print(json.dumps(r), flush=True)
+                for split in (True, False):
+                    r = time_prefill_gemm(f, R, K, split=split)
+                    r["shape"] = name
+                    print(json.dumps(r), flush=True)
         sys.exit(0)
     fmts = sys.argv[1:] or ["i4g32", "i4", "i8", "f16"]
     for f in fmts:

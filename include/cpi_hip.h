@@ -231,7 +231,16 @@ int cpi_hip_attention_prefill_window(const uint16_t* q, const uint16_t* k_cache,
  *                                k/v rows go to the cache at positions
  *                                start_position + m
  *   Preconditions: in_features % 64 == 0.
+ *   workspace (optional, device memory): with it the k loop is split over
+ *   several workgroups per output tile when the tile count alone would not
+ *   fill the GPU; the slice partials are summed in a fixed order, so results
+ *   do not depend on it being present.  Its first
+ *   CPI_PREFILL_COUNTER_BYTES must be zero before the first call (every call
+ *   leaves them zero); calls sharing one workspace must not overlap.  A
+ *   smaller workspace than cpi_hip_prefill_gemm_workspace_bytes reports
+ *   selects fewer slices.
  * ---------------------------------------------------------------------- */
+#define CPI_PREFILL_COUNTER_BYTES 16384
 typedef struct cpi_gemm_desc {
   int wfmt;
   const void* w;
@@ -251,9 +260,15 @@ typedef struct cpi_gemm_desc {
   uint16_t* k_cache;
   uint16_t* v_cache;
   int max_context;
+  /* split-K workspace (may be null) */
+  void* workspace;
+  size_t workspace_bytes;
 } cpi_gemm_desc;
 
 int cpi_hip_prefill_gemm(const cpi_gemm_desc* d, cpi_stream_t stream);
+/* Workspace bytes at which cpi_hip_prefill_gemm uses its full split for this
+ * shape (0: the shape does not split). */
+size_t cpi_hip_prefill_gemm_workspace_bytes(int out_features, int in_features, int num_tokens);
 
 /* ------------------------------------------------------------------------
  * Fused decode step: one persistent launch per token runs the embedding, all

@@ -18,14 +18,25 @@ if torch.cuda.is_available():
     from tests.test_gpu_kernels import FMTS, make_weights, _split_rows
 
 
-def gemm(fmt, w, s, sc_count, N, K, x16, M, y, epilogue=_lib.EPI_STORE_F32, **kw):
+def workspace(N, K, M):
+    """Zeroed split-K workspace of the size the library asks for (None when
+    the shape does not split)."""
+    nbytes = _lib.lib().cpi_hip_prefill_gemm_workspace_bytes(N, K, M)
+    return G.dev(np.zeros(nbytes, np.uint8)) if nbytes else None
+
+
+def gemm(fmt, w, s, sc_count, N, K, x16, M, y, epilogue=_lib.EPI_STORE_F32, split=True, **kw):
     d = _lib.GemmDesc()
+    ws = workspace(N, K, M) if split else None
+    if ws is not None:
+        d.workspace, d.workspace_bytes = G.ptr(ws), ws.numel()
     d.wfmt, d.w, d.scales, d.scale_count = FMTS[fmt], G.ptr(w), G.ptr(s), sc_count
     d.out_features, d.in_features, d.x, d.num_tokens = N, K, G.ptr(x16), M
     d.epilogue, d.y = epilogue, G.ptr(y)
     for k, v in kw.items():
         setattr(d, k, G.ptr(v) if isinstance(v, torch.Tensor) else v)
     _lib.call("cpi_hip_prefill_gemm", ctypes.byref(d), G.stream())
+    return ws
 
 
 def row_bound(fmt, deq, x):
@@ -35,18 +46,27 @@ def row_bound(fmt, deq, x):
     return c * np.sqrt((x.astype(np.float64) ** 2) @ (deq.astype(np.float64) ** 2).T) + 1e-5
 
 
+@pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("fmt", ["f16", "i8", "i4", "i4g32"])
 @pytest.mark.parametrize("N,K,M", [(64, 64, 1), (200, 192, 7), (384, 512, 64), (1000, 1024, 130),
                                    (4096, 11008, 128)])
-def test_prefill_gemm_parity(fmt, N, K, M):
-    print(f"[pgemm] fmt={fmt} N={N} K={K} M={M}", flush=True)
+def test_prefill_gemm_parity(fmt, N, K, M, split):
+    print(f"[pgemm] fmt={fmt} N={N} K={K} M={M} split={split}", flush=True)
     blob, sc, deq = make_weights(fmt, N, K, N + K + M, random_lowbit=(N >= 4096))
     x16 = np.random.default_rng(M).standard_normal((M, K)).astype(np.float16)
     xf = x16.astype(np.float32)
     y = G.empty(M * N * 4)
-    gemm(fmt, G.dev(blob), None if sc is None else G.dev(sc), 0 if sc is None else sc.size, N, K,
-         G.dev(x16), M, y)
+    wd, sd, xd = G.dev(blob), None if sc is None else G.dev(sc), G.dev(x16)
+    ws = gemm(fmt, wd, sd, 0 if sc is None else sc.size, N, K, xd, M, y, split=split)
     got = G.host(y, np.float32, M * N).reshape(M, N)
+    if ws is not None:
+        # the counters are back at zero, and a second call (arrival order may
+        # differ) gives the same bits: slices are summed in slice order
+        cnt = G.host(ws, np.uint32, _lib.PREFILL_COUNTER_BYTES // 4)
+        assert not np.any(cnt)
+        y2 = G.empty(M * N * 4)
+        gemm(fmt, wd, sd, 0 if sc is None else sc.size, N, K, xd, M, y2, split=split)
+        assert np.array_equal(G.host(y2, np.float32, M * N).reshape(M, N), got)
     rows = [0, M // 2, M - 1]
     ref = np.stack([oracle.gemv(fmt, blob, sc, N, K, xf[m]) for m in rows])
     bound = row_bound(fmt, deq, xf[rows])
@@ -71,8 +91,8 @@ def test_prefill_gemm_global_scale_and_resid():
 
 
 @pytest.mark.parametrize("fmt", ["f16", "i4g32"])
-def test_prefill_gemm_swiglu(fmt):
-    I, H, M = 320, 256, 33
+@pytest.mark.parametrize("I,H,M", [(320, 256, 33), (512, 1024, 128)])
+def test_prefill_gemm_swiglu(fmt, I, H, M):
     blob, sc, deq = make_weights(fmt, 2 * I, H, 9)
     order = np.zeros(2 * I, np.int32)
     _lib.call("cpi_hip_swiglu_row_order", I, order.ctypes.data_as(ctypes.POINTER(ctypes.c_int)))
