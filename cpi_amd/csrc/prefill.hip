@@ -48,6 +48,46 @@ __global__ void __launch_bounds__(256) rmsnorm_rows_kernel(const float* x, const
   for (int i = threadIdx.x; i < cols; i += 256) yr[i] = f2h((inv * xr[i]) * h2f(w[i]));
 }
 
+// Same result for cols % 4 == 0 and cols <= 1024 V: the row is read once, in
+// 16-byte vectors held in registers, and written as 8-byte fp16 quads.
+template <int V>
+__global__ void __launch_bounds__(256) rmsnorm_rows_vec_kernel(const float* x, const uint16_t* w, uint16_t* y,
+                                                               int cols, float eps) {
+  __shared__ float red[4];
+  const int nq = cols / 4;
+  const f4* xr = reinterpret_cast<const f4*>(x + static_cast<size_t>(blockIdx.x) * cols);
+  uint2* yr = reinterpret_cast<uint2*>(y + static_cast<size_t>(blockIdx.x) * cols);
+  const uint2* wq = reinterpret_cast<const uint2*>(w);
+  f4 v[V];
+  uint2 wv[V];
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int q = threadIdx.x + 256 * k;
+    if (q < nq) {
+      v[k] = xr[q];
+      wv[k] = wq[q];
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < V; ++k)
+    if (threadIdx.x + 256 * k < nq) ss += v[k].x * v[k].x + v[k].y * v[k].y + v[k].z * v[k].z + v[k].w * v[k].w;
+  ss = block_sum(ss, red);
+  const float inv = 1.f / sqrtf(ss / static_cast<float>(cols) + eps);
+#pragma unroll
+  for (int k = 0; k < V; ++k) {
+    const int q = threadIdx.x + 256 * k;
+    if (q < nq) {
+      const f16x2 w01 = as_h2(wv[k].x), w23 = as_h2(wv[k].y);
+      const uint32_t lo = static_cast<uint32_t>(f2h((inv * v[k].x) * static_cast<float>(w01.x))) |
+                          (static_cast<uint32_t>(f2h((inv * v[k].y) * static_cast<float>(w01.y))) << 16);
+      const uint32_t hi = static_cast<uint32_t>(f2h((inv * v[k].z) * static_cast<float>(w23.x))) |
+                          (static_cast<uint32_t>(f2h((inv * v[k].w) * static_cast<float>(w23.y))) << 16);
+      yr[q] = uint2{lo, hi};
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // GEMM  Y[m, n] = sum_k X[m, k] W[n, k]  (W row-major [N, K] in a CPI_W_*
 // format, X fp16 [M, K]) with the engine's fused epilogues.
@@ -513,33 +553,68 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(APParams p) {
 
   const uint16_t* kb = p.k + kvh * HD;
   const uint16_t* vb = p.v + kvh * HD;
-  for (int kt = kbeg; kt < kend; kt += 32) {
-    __syncthreads();  // previous step's readers are done with the tiles
-    // K tile: 32 keys x HD, 16-byte pieces
-    for (int u = t; u < 32 * (HD / 8); u += 256) {
-      const int key = u / (HD / 8), piece = u % (HD / 8);
-      const int kp = min(kt + key, kend - 1);
-      *reinterpret_cast<u32x4*>(&Ks[key * KLd + 8 * piece]) =
-          *reinterpret_cast<const u32x4*>(kb + static_cast<size_t>(kp) * kvdim + 8 * piece);
-    }
-    // V^T tile: units of (2 keys, 8 dims)
-    for (int u = t; u < 16 * (HD / 8); u += 256) {
-      const int kpair = u / (HD / 8), piece = u % (HD / 8);
-      const int kp0 = min(kt + 2 * kpair, kend - 1), kp1 = min(kt + 2 * kpair + 1, kend - 1);
-      const u32x4 a = *reinterpret_cast<const u32x4*>(vb + static_cast<size_t>(kp0) * kvdim + 8 * piece);
-      const u32x4 b = *reinterpret_cast<const u32x4*>(vb + static_cast<size_t>(kp1) * kvdim + 8 * piece);
-      const uint32_t ad[4] = {a.x, a.y, a.z, a.w}, bd[4] = {b.x, b.y, b.z, b.w};
+  // K/V tiles of a 32-key step pass through registers: thread t loads K
+  // pieces u = t + 256 i (key u / (HD/8), 8 dims) and V pairs u = t + 256 i
+  // (keys 2 (u / (HD/8)) + {0,1}).  Two register sets: the tiles of step
+  // n + 2 are requested while step n computes.
+  constexpr int KU = (32 * (HD / 8) + 255) / 256;
+  constexpr int VU = (16 * (HD / 8) + 255) / 256;
+  struct KV {
+    u32x4 k[KU], va[VU], vb[VU];
+  };
+  auto load_kv = [&](KV& r, int kt) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        // dims 8*piece + 2i (low halves) and + 2i + 1 (high halves)
-        *reinterpret_cast<uint32_t*>(&Vt[(8 * piece + 2 * i) * VLd + 2 * kpair]) =
-            __builtin_amdgcn_perm(bd[i], ad[i], 0x05040100u);
-        *reinterpret_cast<uint32_t*>(&Vt[(8 * piece + 2 * i + 1) * VLd + 2 * kpair]) =
-            __builtin_amdgcn_perm(bd[i], ad[i], 0x07060302u);
+    for (int i = 0; i < KU; ++i) {
+      const int u = t + 256 * i;
+      if (u < 32 * (HD / 8)) {
+        const int key = u / (HD / 8), piece = u % (HD / 8);
+        const int kp = min(kt + key, kend - 1);
+        r.k[i] = *reinterpret_cast<const u32x4*>(kb + static_cast<size_t>(kp) * kvdim + 8 * piece);
       }
     }
-    __syncthreads();
-
+#pragma unroll
+    for (int i = 0; i < VU; ++i) {
+      const int u = t + 256 * i;
+      if (u < 16 * (HD / 8)) {
+        const int kpair = u / (HD / 8), piece = u % (HD / 8);
+        const int kp0 = min(kt + 2 * kpair, kend - 1), kp1 = min(kt + 2 * kpair + 1, kend - 1);
+        r.va[i] = *reinterpret_cast<const u32x4*>(vb + static_cast<size_t>(kp0) * kvdim + 8 * piece);
+        r.vb[i] = *reinterpret_cast<const u32x4*>(vb + static_cast<size_t>(kp1) * kvdim + 8 * piece);
+      }
+    }
+  };
+  auto store_kv = [&](const KV& r) {
+#pragma unroll
+    for (int i = 0; i < KU; ++i) {
+      const int u = t + 256 * i;
+      if (u < 32 * (HD / 8)) {
+        const int key = u / (HD / 8), piece = u % (HD / 8);
+        *reinterpret_cast<u32x4*>(&Ks[key * KLd + 8 * piece]) = r.k[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < VU; ++i) {
+      const int u = t + 256 * i;
+      if (u < 16 * (HD / 8)) {
+        const int kpair = u / (HD / 8), piece = u % (HD / 8);
+        const uint32_t ad[4] = {r.va[i].x, r.va[i].y, r.va[i].z, r.va[i].w};
+        const uint32_t bd[4] = {r.vb[i].x, r.vb[i].y, r.vb[i].z, r.vb[i].w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          // dims 8*piece + 2q (low halves) and + 2q + 1 (high halves)
+          *reinterpret_cast<uint32_t*>(&Vt[(8 * piece + 2 * q) * VLd + 2 * kpair]) =
+              __builtin_amdgcn_perm(bd[q], ad[q], 0x05040100u);
+          *reinterpret_cast<uint32_t*>(&Vt[(8 * piece + 2 * q + 1) * VLd + 2 * kpair]) =
+              __builtin_amdgcn_perm(bd[q], ad[q], 0x07060302u);
+        }
+      }
+    }
+  };
+  const int klast = kend - 1 > kbeg ? ((kend - 1) & ~31) : kbeg;  // start of the last step
+  auto cl = [&](int kt) { return kt < klast ? kt : klast; };
+  // One 32-key step from the staged tiles.  A step whose keys are all masked
+  // (past the tile's last key) leaves the running state unchanged.
+  auto compute = [&](int kt) {
     // S^T for keys kt + [0,16) and kt + [16,32)
     f4 sb[2];
 #pragma unroll
@@ -586,6 +661,24 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(APParams p) {
       o[d] = o[d] * alpha;
       o[d] = mfma16(__builtin_bit_cast(h8, vv), pf, o[d]);
     }
+  };
+  KV r0, r1;
+  load_kv(r0, kbeg);
+  load_kv(r1, cl(kbeg + 32));
+  __builtin_amdgcn_sched_barrier(0);
+  for (int kt = kbeg; kt < kend; kt += 64) {
+    lds_barrier();  // previous step's readers are done with the tiles
+    store_kv(r0);
+    load_kv(r0, cl(kt + 64));
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    compute(kt);
+    lds_barrier();
+    store_kv(r1);
+    load_kv(r1, cl(kt + 96));
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    compute(kt + 32);
   }
 
   if (qvalid) {
@@ -603,7 +696,14 @@ __global__ void __launch_bounds__(256) attn_prefill_kernel(APParams p) {
 // ---------------------------------------------------------------------------
 hipError_t rmsnorm_rows_launch(const float* x, const uint16_t* w, uint16_t* y, int rows, int cols, float eps,
                                hipStream_t s) {
-  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, s, x, w, y, cols, eps);
+  const bool vec = cols % 4 == 0 && ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(w) |
+                                       reinterpret_cast<uintptr_t>(y)) & 15) == 0;
+  if (vec && cols <= 1024 * 4)
+    hipLaunchKernelGGL(rmsnorm_rows_vec_kernel<4>, dim3(rows), dim3(256), 0, s, x, w, y, cols, eps);
+  else if (vec && cols <= 1024 * 8)
+    hipLaunchKernelGGL(rmsnorm_rows_vec_kernel<8>, dim3(rows), dim3(256), 0, s, x, w, y, cols, eps);
+  else
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, s, x, w, y, cols, eps);
   return hipGetLastError();
 }
 

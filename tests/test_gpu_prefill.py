@@ -173,3 +173,25 @@ def test_prefill_rejects_bad_shapes():
     assert _lib.lib().cpi_hip_prefill_gemm(ctypes.byref(d), G.stream()) == -1  # K % 64
     assert _lib.lib().cpi_hip_attention_prefill(G.ptr(x), G.ptr(x), G.ptr(x), G.ptr(x), 1, 0, 4, 4, 96,
                                                 G.stream()) == -1  # head_dim
+
+
+@pytest.mark.parametrize("rows,cols,offset", [(128, 4096, 0), (7, 11008, 0), (3, 8192, 0), (5, 16384, 0),
+                                              (4, 4098, 0), (6, 512, 1)])
+def test_rmsnorm_rows_matches_oracle(rows, cols, offset):
+    """Per-row RMSNorm of fp32 rows into fp16 (vectorised kernel for
+    cols % 4 == 0 up to 8192 with 16-byte aligned pointers, scalar otherwise;
+    offset = 1 float misaligns x to take the scalar path)."""
+    print(f"[rmsnorm_rows] rows={rows} cols={cols} offset={offset}", flush=True)
+    rng = np.random.default_rng(cols + rows)
+    x = rng.standard_normal((rows, cols)).astype(np.float32) * 3
+    w = (rng.standard_normal(cols) * 0.5 + 1).astype(np.float16)
+    xd = G.dev(np.concatenate([np.zeros(offset, np.float32), x.ravel()]))
+    y = G.empty(rows * cols * 2)
+    wd = G.dev(w)
+    _lib.call("cpi_hip_rmsnorm_rows_f32", ctypes.c_void_p(xd.data_ptr() + 4 * offset), G.ptr(wd), G.ptr(y), rows, cols,
+              ctypes.c_float(1e-5), G.stream())
+    got = G.host(y, np.float16, rows * cols).reshape(rows, cols).astype(np.float32)
+    for r in range(rows):
+        ref = oracle.rmsnorm(x[r], w, 1e-5)
+        # fp32 statistics in a different summation order, then one fp16 rounding
+        np.testing.assert_allclose(got[r], ref.astype(np.float16).astype(np.float32), rtol=2e-3, atol=1e-3)
