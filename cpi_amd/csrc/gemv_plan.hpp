@@ -80,10 +80,14 @@ CPI_HD inline bool plan_valid(int shape, int ks) {
   return nr * kWavesPerBlock % ks == 0 && rb >= kTileRows && rb % kTileRows == 0;
 }
 
-// Host plan: all loads of a wave in flight at once where the shape allows,
-// full pass utilisation, and enough waves (>= 2 per SIMD of 256 CUs) to fill
-// the chip; `slots` launches of the plan run side by side (grid.y, gathered
-// MoE experts).  force_shape / force_ks (>= 0 / > 0) override the choice.
+// Host plan: full pass utilisation first, then enough waves to keep HBM busy
+// (1024 waves x slots saturate it at batch 1), then many rows per wave (each
+// prepared activation read from LDS serves NR rows).  Ties go to more waves.
+// `slots` launches of the plan run side by side (grid.y, gathered MoE
+// experts).  force_shape / force_ks (>= 0 / > 0) override the choice.
+// Measured on MI355X (int4-g32, Llama-2-7B / Mixtral shapes): (8, 1) with
+// ks = 2 is the fastest or within 2 % for QKV, w1|w3, w2, o_proj and the
+// gathered expert w2 (20 -> 14.6 us).
 inline GemvPlan plan_launch(int R, int K, int elems, int force_shape, int force_ks, int slots = 1) {
   double best = -1.0;
   GemvPlan bp = make_plan(R, K, elems, 0, 1);
@@ -95,11 +99,11 @@ inline GemvPlan plan_launch(int R, int K, int elems, int force_shape, int force_
       const GemvPlan g = make_plan(R, K, elems, s, ks);
       const double util = static_cast<double>(g.np) / (static_cast<double>(g.ks) * g.ng * g.pp);
       const double waves = static_cast<double>(g.grid) * kWavesPerBlock * slots;
-      double score = util * (waves >= 2048.0 ? 1.0 : waves / 2048.0);
-      if (g.ng > 1) score *= 0.9;
+      double score = util * (waves >= 1024.0 ? 1.0 : waves / 1024.0);
+      score *= g.nr >= 8 ? 1.0 : (g.nr >= 4 ? 0.95 : 0.85);
       if (g.nr * g.pp < 8) score *= 0.9;
-      // ties: more bytes per wave in flight, then more rows per wave
-      score += 1e-3 * g.nr * g.pp + 1e-4 * g.nr;
+      // ties: more waves, then more rows per wave
+      score += 1e-3 * (waves < 8192.0 ? waves : 8192.0) / 8192.0 + 1e-4 * g.nr;
       if (score > best) {
         best = score;
         bp = g;

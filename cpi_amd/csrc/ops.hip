@@ -95,48 +95,64 @@ __global__ void scale_add_kernel(uint16_t* dst, const uint16_t* src, int n, floa
 
 // ---- MoE router: softmax over experts, greedy top-k with strict '>',
 //      renormalised over the picked experts (kernels_ops_matvec.cu:115-193,
-//      cpu_engine.cpp:560-606).  Single thread: experts <= 64.
-__device__ void topk_softmax(const float* lg, int experts, int top_k, int* idx, float* prob) {
-  float pr[64];
-  float mx = lg[0];
-  for (int e = 1; e < experts; ++e) mx = fmaxf(mx, lg[e]);
+//      cpu_engine.cpp:560-606).  One wave, lane e holding expert e's logit
+//      (experts <= 64); everything stays in registers.  The arithmetic and its
+//      order are those of the sequential loop: the max is order-free, the
+//      exponentials are summed in expert order (readlane), and each pick is
+//      the highest unused probability with the lowest expert index among
+//      equals, which is what a strict '>' scan in expert order selects.
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ void topk_softmax_wave(float lgv, int experts, int top_k, int* idx, float* prob) {
+  const int lane = threadIdx.x & 63;
+  const bool live = lane < experts;
+  float mx = live ? lgv : -__builtin_inff();
+  mx = wave_max(mx);
+  const float ex = live ? expf(lgv - mx) : 0.f;
   float sum = 0.f;
-  for (int e = 0; e < experts; ++e) {
-    pr[e] = expf(lg[e] - mx);
-    sum += pr[e];
-  }
+  for (int e = 0; e < experts; ++e) sum += lane_f(ex, e);
   const float inv = 1.f / fmaxf(sum, 1e-8f);
-  for (int e = 0; e < experts; ++e) pr[e] *= inv;
-  unsigned long long used = 0;
+  const float pr = ex * inv;
+  bool used = !live;
+  const int kk = top_k < 8 ? top_k : 8;
   int pick[8];
   float pp[8];
-  const int kk = top_k < 8 ? top_k : 8;
   float psum = 0.f;
-  for (int k = 0; k < kk; ++k) {
-    int best = -1;
-    float bp = -1.f;
-    for (int e = 0; e < experts; ++e) {
-      if (used & (1ull << e)) continue;
-      if (pr[e] > bp) { bp = pr[e]; best = e; }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    pick[k] = 0;
+    pp[k] = 0.f;
+    if (k < kk) {
+      const float cand = used ? -1.f : pr;
+      const float bp = wave_max(cand);
+      const unsigned long long at = __ballot(!used && cand == bp);
+      const int best = bp > -1.f && at != 0ull ? __builtin_ctzll(at) : -1;
+      pick[k] = best < 0 ? 0 : best;
+      pp[k] = bp > 0.f ? bp : 0.f;
+      if (lane == best) used = true;
+      psum += pp[k];
     }
-    pick[k] = best < 0 ? 0 : best;
-    pp[k] = bp > 0.f ? bp : 0.f;
-    if (best >= 0) used |= 1ull << best;
-    psum += pp[k];
   }
   const float ip = 1.f / fmaxf(psum, 1e-8f);
-  for (int k = 0; k < top_k; ++k) {
-    idx[k] = k < kk ? pick[k] : 0;
-    prob[k] = k < kk ? pp[k] * ip : 0.f;
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k)
+      if (k < top_k) {
+        idx[k] = k < kk ? pick[k] : 0;
+        prob[k] = k < kk ? pp[k] * ip : 0.f;
+      }
+    for (int k = 8; k < top_k; ++k) {
+      idx[k] = 0;
+      prob[k] = 0.f;
+    }
   }
 }
 
 __global__ void router_topk_kernel(const uint16_t* logits, int experts, int top_k, int* idx,
                                    float* prob) {
-  if (threadIdx.x != 0) return;
-  float lg[64];
-  for (int e = 0; e < experts; ++e) lg[e] = h2f(logits[e]);
-  topk_softmax(lg, experts, top_k, idx, prob);
+  const int lane = threadIdx.x & 63;
+  topk_softmax_wave(lane < experts ? h2f(logits[lane]) : 0.f, experts, top_k, idx, prob);
 }
 
 // ---- Fused decode router: RMSNorm of the fp32 residual (fp32 statistics,
@@ -218,10 +234,9 @@ __global__ void __launch_bounds__(kRouterThreads) moe_router_kernel(const float*
     if (lane == 0) lg[e] = d;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    if (logits_out)
-      for (int e = 0; e < experts; ++e) logits_out[e] = lg[e];
-    topk_softmax(lg, experts, top_k, idx, prob);
+  if (wave == 0) {
+    if (logits_out && lane < experts) logits_out[lane] = lg[lane];
+    topk_softmax_wave(lane < experts ? lg[lane] : 0.f, experts, top_k, idx, prob);
   }
 }
 

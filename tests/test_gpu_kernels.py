@@ -407,3 +407,34 @@ def test_gemv_folded_moe_residual(add_k):
     G.gemv(_lib.W_I4G32, w, s, sc.size, R, K, G.dev(x), got, norm_w=nd, add_y=yd, add_p=pd, add_k=add_k, x_out=xo)
     np.testing.assert_array_equal(G.host(xo, np.float32, K), G.host(xr, np.float32, K))
     np.testing.assert_array_equal(G.host(got, np.float32, R), G.host(ref, np.float32, R))
+
+
+@pytest.mark.parametrize("case", ["ties", "e64k8", "e8k2", "e3k3"])
+def test_router_topk_matches_oracle_exactly(case):
+    """Top-k softmax over fp16 logits (one wave, lane = expert) against the
+    oracle's sequential loop: same picks, ties to the lowest expert index
+    (strict '>' scan), and the probabilities to a couple of ulps."""
+    print(f"[router_topk] {case}", flush=True)
+    rng = np.random.default_rng(len(case))
+    if case == "ties":
+        logits = np.array([0.5, 1.25, 1.25, -2.0, 1.25, 0.0, 1.25, 0.5], np.float16)
+        k = 3
+    elif case == "e64k8":
+        logits = rng.standard_normal(64).astype(np.float16)
+        logits[[5, 40]] = logits[17]  # a three-way tie among the large ones
+        logits[17] = logits[5] = logits[40] = np.float16(2.5)
+        k = 8
+    elif case == "e8k2":
+        logits = rng.standard_normal(8).astype(np.float16)
+        k = 2
+    else:
+        logits = rng.standard_normal(3).astype(np.float16)
+        k = 3
+    s = G.stream()
+    idx, pr = G.empty(64), G.empty(64)
+    _lib.call("cpi_hip_moe_router_topk_softmax", G.ptr(G.dev(logits)), logits.size, k, G.ptr(idx), G.ptr(pr), s)
+    ridx, rpr = oracle.router_topk(logits.astype(np.float32), k)
+    assert list(G.host(idx, np.int32, k)) == list(ridx)
+    np.testing.assert_allclose(G.host(pr, np.float32, k), rpr, rtol=1e-6, atol=1e-7)
+    if case == "ties":
+        assert list(ridx) == [1, 2, 4]
