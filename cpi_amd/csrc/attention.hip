@@ -14,6 +14,8 @@
 // workgroup and shared by the G query heads of the group; the number of
 // splits is fixed per launch (graph friendly) and the split length adapts to
 // the live sequence length read from device memory.
+#include <cstdlib>
+
 #include "common.hpp"
 #include "../../include/cpi_hip.h"
 
@@ -31,6 +33,7 @@ struct AttnParams {
   const int* position;  // seq = *position + 1
   int nh, nkv, max_ctx, window;
   int nsplit;
+  int minchunk;         // shortest split in tokens (a multiple of the workgroup step)
   float scale;          // log2(e) / sqrt(head_dim): scores in base-2 units
   float* scratch;       // [nh][MAXS][2] m,l  then [nh][MAXS][hd] o
 };
@@ -74,6 +77,7 @@ __device__ __forceinline__ SplitGeom split_geom(const AttnParams& p) {
   sg.start = (p.window > 0 && seq > p.window) ? seq - p.window : 0;
   const int len = seq - sg.start;
   int chunk = (len + p.nsplit - 1) / p.nsplit;
+  if (chunk < p.minchunk) chunk = p.minchunk;  // 0 in callers without a minimum
   chunk = ((chunk + MINCHUNK - 1) / MINCHUNK) * MINCHUNK;
   if (chunk < MINCHUNK) chunk = MINCHUNK;
   sg.chunk = chunk;
@@ -408,12 +412,31 @@ hipError_t launch_hd(const AttnParams& p, int G, bool qf32, bool of32, hipStream
 
 }  // namespace
 
-// Split count: enough workgroups to cover the 256 CUs several times at long
-// context, bounded by the scratch capacity.
+// Split count: 256 workgroups over all KV heads at long context (one per CU),
+// bounded by the scratch capacity.  Measured on MI355X (32 q / 8 kv heads,
+// hd 128): 256 beats 512 at every context (4096: 18.9 -> 14.0 us, 32768:
+// 39.3 -> 33.6 us; 512 unchanged at 7.7 us) and 128 loses at 32768.
+// CPI_ATTN_SPLITS (tuning) overrides the total.
 int attn_num_splits(int nkv) {
-  int n = 512 / (nkv > 0 ? nkv : 1);
+  static const int total = [] {
+    const char* v = std::getenv("CPI_ATTN_SPLITS");
+    const int n = v ? std::atoi(v) : 0;
+    return n > 0 ? n : 256;
+  }();
+  int n = total / (nkv > 0 ? nkv : 1);
   if (n < 1) n = 1;
   if (n > CPI_ATTN_MAX_SPLITS) n = CPI_ATTN_MAX_SPLITS;
+  return n;
+}
+
+// Shortest split: a split shorter than this costs more in its merge than it
+// saves in parallelism.  CPI_ATTN_MINCHUNK (tuning) overrides.
+int attn_min_chunk() {
+  static const int n = [] {
+    const char* v = std::getenv("CPI_ATTN_MINCHUNK");
+    const int m = v ? std::atoi(v) : 0;
+    return m > 0 ? m : 1;
+  }();
   return n;
 }
 
@@ -431,6 +454,7 @@ hipError_t attn_launch(const void* q, bool qf32, const uint16_t* k, const uint16
   p.seq_len = seq_len; p.position = position;
   p.nh = nh; p.nkv = nkv; p.max_ctx = max_ctx; p.window = window;
   p.nsplit = attn_num_splits(nkv);
+  p.minchunk = attn_min_chunk();
   p.scale = 1.4426950408889634f / sqrtf(static_cast<float>(hd));  // log2(e) / sqrt(hd)
   p.scratch = scratch;
   const int G = nh / nkv;
