@@ -214,3 +214,31 @@ def test_tinyllama_golden(tmp_path):
     print(f"[tinyllama] max_abs_logit_err={err:.3e} identical_prefix={n}/64", flush=True)
     assert err <= LOGIT_TOL
     assert n >= 32, "TinyLlama config-1 ids must match for 32 steps"
+
+
+@pytest.mark.parametrize("quant", ["int4-g32", "int8"])
+def test_converted_hf_checkpoint(tmp_path, quant):
+    """An HF-format checkpoint (safetensors + config.json) converted by
+    `cpi_amd.ll2c_tools convert` with every projection quantised runs in the
+    resident engine with the oracle's greedy ids and logits."""
+    from cpi_amd import ll2c_tools
+    from cpi_amd.engine_py import Engine
+    from tests.test_ll2c_tools import hf_tensors, make_hf
+    cfg = dict(model_type="llama", vocab_size=300, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+               num_attention_heads=4, num_key_value_heads=2, max_position_embeddings=128, rms_norm_eps=1e-5)
+    print(f"[engine] converted HF checkpoint quant={quant}", flush=True)
+    make_hf(tmp_path / "hf", cfg, hf_tensors(cfg, np.random.default_rng(5), "BF16"), shards=2)
+    path = str(tmp_path / "conv.ll2c")
+    assert ll2c_tools.main(["convert", "--hf-dir", str(tmp_path / "hf"), "--output", path, "--quant", quant,
+                            "--quant-scope", "all", "--omit-fp16"]) == 0
+    ll2c_tools.validate(path)
+    prompt = np.random.default_rng(2).integers(0, 300, 21)
+    rids, rlg = oracle.Engine(path, 96).generate(prompt, 32, eos=-1, logit_steps=32)
+    eng = Engine(path, max_context=96, eos=-1, loop_guard=False)
+    ids, lg = eng.generate(prompt, 32, logit_steps=32)
+    eng.close()
+    n = first_divergence(ids, rids)
+    err = np.abs(lg[:n] - rlg[:n]).max()
+    print(f"[engine] converted {quant}: max_abs_logit_err={err:.3e} identical_prefix={n}/32", flush=True)
+    assert err <= LOGIT_TOL
+    assert_ids_or_tie(n, rlg, err)
