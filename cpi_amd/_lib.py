@@ -44,6 +44,12 @@ class GemmDesc(ctypes.Structure):
     ]
 
 
+class SamplingParams(ctypes.Structure):
+    """Mirror of cpi_sampling_params."""
+    _fields_ = [("temperature", ctypes.c_float), ("top_k", c_int), ("top_p", ctypes.c_float),
+                ("repetition_penalty", ctypes.c_float), ("no_repeat_ngram_size", c_int)]
+
+
 W_F16, W_I8ROW, W_I4ROW, W_I4G32 = 0, 1, 2, 3
 EPI_STORE_F32, EPI_STORE_F16, EPI_RESID_ADD, EPI_SWIGLU, EPI_QKV_ROPE, EPI_SWIGLU_F16 = 0, 1, 2, 3, 4, 5
 ATTN_MAX_SPLITS = 256
@@ -72,6 +78,8 @@ _SIGS = {
     "cpi_hip_attention_prefill": (c_int, [c_void_p] * 4 + [c_int] * 5 + [c_void_p]),
     "cpi_hip_attention_prefill_window": (c_int, [c_void_p] * 4 + [c_int] * 6 + [c_void_p]),
     "cpi_hip_prefill_gemm": (c_int, [ctypes.POINTER(GemmDesc), c_void_p]),
+    "cpi_hip_sample_advance": (c_int, [c_void_p, c_int, ctypes.POINTER(SamplingParams), c_void_p, c_int, c_void_p,
+                                       c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
     "cpi_hip_prefill_gemm_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
     "cpi_hip_rmsnorm_rows_f32": (c_int, [c_void_p] * 3 + [c_int, c_int, c_float, c_void_p]),
     "cpi_hip_decode_fused_supported": (c_int, [c_void_p]),

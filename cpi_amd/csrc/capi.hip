@@ -14,6 +14,7 @@
 #include "ops.hip"
 #include "prefill.hip"
 #include "decode_fused.hip"
+#include "sampling.hip"
 
 namespace {
 
@@ -412,6 +413,25 @@ int cpi_hip_greedy_advance(const float* logits, int n, int* token, int* position
   hipLaunchKernelGGL(cpi::argmax_advance_kernel, dim3(1), dim3(1024), 0, S(s), logits, n, token,
                      position, step, ring, ring_len);
   return check(hipGetLastError(), "greedy_advance");
+}
+
+int cpi_hip_sample_advance(const float* logits, int vocab, const cpi_sampling_params* params, const float* rand,
+                           int rand_len, uint32_t* seen, int* history, int history_cap, int* token, int* position,
+                           int* step, int* ring, int ring_len, cpi_stream_t s) {
+  if (!logits || !params || !rand || !token || !position || !step || !ring)
+    return fail("sample_advance: null pointer");
+  if (vocab <= 0 || vocab > cpi::kSampMaxVocab) return fail("sample_advance: vocab must be in [1, 65536]");
+  if (rand_len <= 0 || ring_len <= 0) return fail("sample_advance: rand_len and ring_len must be positive");
+  if (history && history_cap <= 0) return fail("sample_advance: history_cap must be positive");
+  cpi::SampleParams sp;
+  sp.temperature = params->temperature;
+  sp.top_k = params->top_k;
+  sp.top_p = params->top_p;
+  sp.rep_penalty = params->repetition_penalty;
+  sp.ngram = params->no_repeat_ngram_size;
+  return check(cpi::sample_advance_launch(logits, vocab, sp, rand, rand_len, seen, history, history_cap, token,
+                                          position, step, ring, ring_len, S(s)),
+               "sample_advance");
 }
 
 int cpi_hip_prompt_advance(const int* prompt, int n, int* token, int* position, cpi_stream_t s) {

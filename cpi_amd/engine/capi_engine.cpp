@@ -34,6 +34,7 @@ void cpi_engine_default_options(cpi_engine_options* o) {
   o->profile_decode_phases = 0;
   o->graph_steps = d.graph_steps;
   o->prefill_chunk = d.prefill_chunk;
+  o->no_repeat_ngram_size = d.no_repeat_ngram_size;
 }
 
 const char* cpi_engine_last_error(void) { return g_err.c_str(); }
@@ -58,6 +59,7 @@ cpi_engine* cpi_engine_create(const cpi_engine_options* o) {
     opt.profile_decode_phases = o->profile_decode_phases != 0;
     opt.graph_steps = o->graph_steps;
     opt.prefill_chunk = o->prefill_chunk;
+    opt.no_repeat_ngram_size = o->no_repeat_ngram_size;
     e->eng.initialize(opt);
   } catch (const std::exception& ex) {
     fail(ex);

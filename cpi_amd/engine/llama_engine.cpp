@@ -14,7 +14,9 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
 #include <iostream>
+#include <limits>
 #include <numeric>
 #include <random>
 #include <stdexcept>
@@ -65,7 +67,8 @@ bool has_degenerate_tail(const std::vector<int>& ids, std::size_t prompt_size) {
 }  // namespace
 
 LlamaEngine::~LlamaEngine() {
-  for (hipGraphExec_t g : {g_decode_many_, g_decode_one_, g_prefill_many_, g_prefill_one_})
+  for (hipGraphExec_t g : {g_decode_many_, g_decode_one_, g_prefill_many_, g_prefill_one_, g_sample_many_,
+                           g_sample_one_})
     if (g) (void)hipGraphExecDestroy(g);
   for (void* p : allocations_) (void)hipFree(p);
   if (stream_) (void)hipStreamDestroy(stream_);
@@ -364,6 +367,15 @@ void LlamaEngine::initialize(const EngineOptions& options) {
   d_step_ = static_cast<int*>(dmalloc(4));
   d_ring_ = static_cast<int*>(dmalloc(static_cast<std::size_t>(ring_len_) * 4));
   prompt_cap_ = opts_.max_context;
+  // device sampler state: draws for one graph launch, seen-id bitmap, history
+  device_sampling_ = V <= 65536;
+  if (device_sampling_) {
+    rand_len_ = std::max(ring_len_, graph_steps_);
+    h_rand_.assign(static_cast<std::size_t>(rand_len_), 0.f);
+    d_rand_ = static_cast<float*>(dmalloc(static_cast<std::size_t>(rand_len_) * 4));
+    d_seen_ = static_cast<uint32_t*>(dmalloc(static_cast<std::size_t>((V + 31) / 32) * 4));
+    d_hist_ = static_cast<int*>(dmalloc(static_cast<std::size_t>(opts_.max_context) * 4));
+  }
   d_prompt_ = static_cast<int*>(dmalloc(static_cast<std::size_t>(prompt_cap_) * 4));
   HIP_OK(hipMemset(d_prompt_, 0, static_cast<std::size_t>(prompt_cap_) * 4));
   HIP_OK(hipMemset(d_token_, 0, 4));
@@ -471,9 +483,9 @@ void LlamaEngine::check_fused() const {
   if (cpi_hip_decode_fused_status(s) != 0) ENGINE_THROW(cpi_hip_last_error_string());
 }
 
-void LlamaEngine::enqueue_step(bool with_head) {
+void LlamaEngine::enqueue_step(bool with_head, const cpi_sampling_params* sampling) {
   const int H = cfg_.hidden_size, I = cfg_.intermediate_size;
-  if (with_head && fused_) {
+  if (with_head && fused_ && !sampling) {
     CPI_OK(cpi_hip_decode_step_fused(&fused_desc_, stream_));
     return;
   }
@@ -566,8 +578,12 @@ void LlamaEngine::enqueue_step(bool with_head) {
     h.norm_w = norm_out_; h.norm_eps = cfg_.norm_eps; h.epilogue = CPI_EPI_STORE_F32; h.y = logits_;
     fold(h, false);
     CPI_OK(cpi_hip_gemv(&h, stream_));
-    CPI_OK(cpi_hip_greedy_advance(logits_, cfg_.vocab_size, d_token_, d_pos_, d_step_, d_ring_, ring_len_,
-                                  stream_));
+    if (sampling)
+      CPI_OK(cpi_hip_sample_advance(logits_, cfg_.vocab_size, sampling, d_rand_, rand_len_, d_seen_, d_hist_,
+                                    opts_.max_context, d_token_, d_pos_, d_step_, d_ring_, ring_len_, stream_));
+    else
+      CPI_OK(cpi_hip_greedy_advance(logits_, cfg_.vocab_size, d_token_, d_pos_, d_step_, d_ring_, ring_len_,
+                                    stream_));
   } else {
     CPI_OK(cpi_hip_prompt_advance(d_prompt_, prompt_cap_, d_token_, d_pos_, stream_));
   }
@@ -632,6 +648,30 @@ void LlamaEngine::build_graphs() {
   g_prefill_many_ = capture(false, graph_steps_);
 }
 
+// Sampled decode graphs for the parameters `sp` (captured again only when the
+// parameters change).
+void LlamaEngine::ensure_sample_graphs(const cpi_sampling_params& sp) {
+  if (g_sample_one_ && std::memcmp(&sp, &sample_params_, sizeof(sp)) == 0) return;
+  for (hipGraphExec_t* g : {&g_sample_one_, &g_sample_many_})
+    if (*g) {
+      HIP_OK(hipGraphExecDestroy(*g));
+      *g = nullptr;
+    }
+  sample_params_ = sp;
+  auto capture = [&](int steps) {
+    hipGraph_t g = nullptr;
+    HIP_OK(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    for (int i = 0; i < steps; ++i) enqueue_step(true, &sample_params_);
+    HIP_OK(hipStreamEndCapture(stream_, &g));
+    hipGraphExec_t ge = nullptr;
+    HIP_OK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+    HIP_OK(hipGraphDestroy(g));
+    return ge;
+  };
+  g_sample_one_ = capture(1);
+  g_sample_many_ = capture(graph_steps_);
+}
+
 void LlamaEngine::run_graph(hipGraphExec_t g) { HIP_OK(hipGraphLaunch(g, stream_)); }
 
 void LlamaEngine::reset_state(const std::vector<int>& prompt) {
@@ -646,6 +686,15 @@ void LlamaEngine::reset_state(const std::vector<int>& prompt) {
   HIP_OK(hipMemcpyAsync(d_pos_, &zero, 4, hipMemcpyHostToDevice, stream_));
   HIP_OK(hipMemcpyAsync(d_step_, &zero, 4, hipMemcpyHostToDevice, stream_));
   if (fused_) HIP_OK(hipMemsetAsync(d_sync_, 0, 64, stream_));  // barrier counters restart at zero
+  if (device_sampling_) {
+    // the sampler's history: the prompt (or the BOS seed) at [0, n), and the
+    // bitmap of its distinct ids
+    std::vector<int> hist = n > 0 ? prompt : std::vector<int>{first};
+    std::vector<uint32_t> bits(static_cast<std::size_t>((cfg_.vocab_size + 31) / 32), 0u);
+    for (int t : hist) bits[static_cast<std::size_t>(t >> 5)] |= 1u << (t & 31);
+    HIP_OK(hipMemcpy(d_hist_, hist.data(), hist.size() * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(d_seen_, bits.data(), bits.size() * 4, hipMemcpyHostToDevice));
+  }
   HIP_OK(hipStreamSynchronize(stream_));
 }
 
@@ -685,20 +734,43 @@ std::vector<int> LlamaEngine::generate_stream(const std::vector<int>& prompt_in,
 
   // ---- decode
   const auto td = Clock::now();
-  const bool greedy = temperature < 1e-6f && opts_.repetition_penalty == 1.0f;
+  // the reference's greedy fast path (llama_engine_sampling.cpp:10-11); every
+  // other setting goes through the sampler, on device when the vocabulary
+  // fits it
+  const bool greedy = temperature <= 0.f && opts_.repetition_penalty <= 1.f && opts_.no_repeat_ngram_size <= 1;
+  const bool dev_sample = !greedy && device_sampling_;
+  if (dev_sample) {
+    cpi_sampling_params sp{};
+    sp.temperature = temperature;
+    sp.top_k = opts_.top_k;
+    sp.top_p = opts_.top_p;
+    sp.repetition_penalty = opts_.repetition_penalty;
+    sp.no_repeat_ngram_size = opts_.no_repeat_ngram_size;
+    ensure_sample_graphs(sp);
+  }
   const bool capture_logits = capture_ != nullptr && capture_steps_ > 0;
   std::vector<int> ring(static_cast<std::size_t>(ring_len_));
-  std::vector<int> history;
+  std::vector<int> history = out;
   int step = 0;
   bool stop = false;
   while (!stop && step < max_new) {
     if (pos >= opts_.max_context) break;
     const int left = std::min(max_new - step, opts_.max_context - pos);
-    const bool batch = greedy && !capture_logits && left >= graph_steps_;
+    const bool on_device = greedy || dev_sample;
+    const bool batch = on_device && !capture_logits && left >= graph_steps_;
     const int n = batch ? graph_steps_ : 1;
-    run_graph(batch ? g_decode_many_ : g_decode_one_);
+    if (dev_sample) {
+      // one uniform draw per token, at the slot of its device step
+      std::uniform_real_distribution<float> dist(0.f, 1.f);
+      for (int i = 0; i < n; ++i) h_rand_[static_cast<std::size_t>((step + i) % rand_len_)] = dist(rng_);
+      HIP_OK(hipMemcpyAsync(d_rand_, h_rand_.data(), static_cast<std::size_t>(rand_len_) * 4, hipMemcpyHostToDevice,
+                            stream_));
+      run_graph(batch ? g_sample_many_ : g_sample_one_);
+    } else {
+      run_graph(batch ? g_decode_many_ : g_decode_one_);
+    }
     int ids[1] = {0};
-    if (greedy) {
+    if (on_device) {
       HIP_OK(hipMemcpyAsync(ring.data(), d_ring_, static_cast<std::size_t>(ring_len_) * 4, hipMemcpyDeviceToHost, stream_));
       HIP_OK(hipStreamSynchronize(stream_));
       if (capture_logits && step < capture_steps_)
@@ -710,7 +782,7 @@ std::vector<int> LlamaEngine::generate_stream(const std::vector<int>& prompt_in,
       HIP_OK(hipMemcpyAsync(d_token_, ids, 4, hipMemcpyHostToDevice, stream_));
     }
     for (int i = 0; i < n && !stop; ++i) {
-      const int tok = greedy ? ring[static_cast<std::size_t>((step) % ring_len_)] : ids[0];
+      const int tok = (greedy || dev_sample) ? ring[static_cast<std::size_t>((step) % ring_len_)] : ids[0];
       ++step;
       ++pos;
       out.push_back(tok);
@@ -727,46 +799,90 @@ std::vector<int> LlamaEngine::generate_stream(const std::vector<int>& prompt_in,
   return out;
 }
 
-// Temperature / top-k / top-p / repetition penalty on host logits
-// (cpu_engine.cpp:709-764; llama_engine_sampling_utils.cpp:10-180).
+// Host sampler for vocabularies beyond the device sampler (> 65536 ids): the
+// steps and float arithmetic of sample_from_logits
+// (llama_engine_sampling_utils.cpp:10-189) with the same draw stream (rng_,
+// one uniform float per token).  Ties in the top-p order go to the lower id.
 int LlamaEngine::sample_host(float temperature, const std::vector<int>& history) {
   const int V = cfg_.vocab_size;
   std::vector<float> lg(static_cast<std::size_t>(V));
   HIP_OK(hipMemcpy(lg.data(), logits_, static_cast<std::size_t>(V) * 4, hipMemcpyDeviceToHost));
+  const float ninf = -std::numeric_limits<float>::infinity();
+  for (float& v : lg) v = std::isfinite(v) ? std::min(std::max(v, -80.f), 80.f) : ninf;
   const float rp = opts_.repetition_penalty;
-  if (rp != 1.0f)
-    for (int id : history)
-      if (id >= 0 && id < V) lg[static_cast<std::size_t>(id)] = lg[static_cast<std::size_t>(id)] > 0.f ? lg[static_cast<std::size_t>(id)] / rp : lg[static_cast<std::size_t>(id)] * rp;
-  if (temperature < 1e-6f) return static_cast<int>(std::max_element(lg.begin(), lg.end()) - lg.begin());
-  for (float& v : lg) v /= temperature;
-  std::vector<int> idx(static_cast<std::size_t>(V));
-  std::iota(idx.begin(), idx.end(), 0);
-  int k = (opts_.top_k > 0 && opts_.top_k < V) ? opts_.top_k : V;
-  std::partial_sort(idx.begin(), idx.begin() + k, idx.end(),
-                    [&](int a, int b) { return lg[static_cast<std::size_t>(a)] > lg[static_cast<std::size_t>(b)]; });
-  idx.resize(static_cast<std::size_t>(k));
-  const float mx = lg[static_cast<std::size_t>(idx[0])];
-  std::vector<double> p(idx.size());
-  double sum = 0.0;
-  for (std::size_t i = 0; i < idx.size(); ++i) sum += p[i] = std::exp(static_cast<double>(lg[static_cast<std::size_t>(idx[i])] - mx));
-  std::size_t keep = idx.size();
-  if (opts_.top_p > 0.f && opts_.top_p < 1.f) {
-    double c = 0.0;
-    for (std::size_t i = 0; i < idx.size(); ++i) {
-      c += p[i] / sum;
-      if (c >= opts_.top_p) { keep = i + 1; break; }
+  if (rp > 1.f && !history.empty()) {
+    std::vector<char> seen(static_cast<std::size_t>(V), 0);
+    for (int id : history) {
+      if (id < 0 || id >= V || seen[static_cast<std::size_t>(id)]) continue;
+      seen[static_cast<std::size_t>(id)] = 1;
+      float& v = lg[static_cast<std::size_t>(id)];
+      v = v > 0.f ? v / rp : v * rp;
     }
   }
-  double s2 = 0.0;
-  for (std::size_t i = 0; i < keep; ++i) s2 += p[i];
-  thread_local std::mt19937 rng{std::random_device{}()};
-  std::uniform_real_distribution<double> dist(0.0, s2);
-  double r = dist(rng), c = 0.0;
-  for (std::size_t i = 0; i < keep; ++i) {
-    c += p[i];
-    if (r <= c) return idx[i];
+  const int ng = opts_.no_repeat_ngram_size;
+  const int hn = static_cast<int>(history.size());
+  if (ng > 1 && hn + 1 >= ng) {
+    std::vector<char> banned(static_cast<std::size_t>(V), 0);
+    for (int i = 0; i + ng <= hn; ++i) {
+      bool match = true;
+      for (int j = 0; j < ng - 1 && match; ++j) match = history[i + j] == history[hn - (ng - 1) + j];
+      const int nx = match ? history[i + ng - 1] : -1;
+      if (nx >= 0 && nx < V) banned[static_cast<std::size_t>(nx)] = 1;
+    }
+    bool cand = false;
+    for (int i = 0; i < V; ++i) {
+      if (banned[static_cast<std::size_t>(i)]) lg[static_cast<std::size_t>(i)] = ninf;
+      else cand |= std::isfinite(lg[static_cast<std::size_t>(i)]);
+    }
+    if (!cand) return 0;
   }
-  return idx[keep - 1];
+  if (temperature <= 0.f) return static_cast<int>(std::max_element(lg.begin(), lg.end()) - lg.begin());
+  const float inv_t = 1.f / temperature;
+  float mx = ninf;
+  for (float& v : lg) {
+    v = v * inv_t;
+    if (std::isfinite(v)) mx = std::max(mx, v);
+  }
+  if (!std::isfinite(mx)) return 0;
+  if (opts_.top_k > 0 && opts_.top_k < V) {
+    std::vector<float> copy = lg;
+    std::nth_element(copy.begin(), copy.begin() + (opts_.top_k - 1), copy.end(), std::greater<float>());
+    const float kth = copy[static_cast<std::size_t>(opts_.top_k - 1)];
+    for (float& v : lg) if (v < kth) v = ninf;
+  }
+  std::vector<float> p(static_cast<std::size_t>(V), 0.f);
+  float sum = 0.f;
+  for (int i = 0; i < V; ++i)
+    if (std::isfinite(lg[static_cast<std::size_t>(i)])) sum += p[static_cast<std::size_t>(i)] = std::exp(lg[static_cast<std::size_t>(i)] - mx);
+  if (!(sum > 0.f)) return 0;
+  for (float& v : p) v /= sum;
+  if (opts_.top_p > 0.f && opts_.top_p < 1.f) {
+    std::vector<int> idx(static_cast<std::size_t>(V));
+    std::iota(idx.begin(), idx.end(), 0);
+    std::stable_sort(idx.begin(), idx.end(), [&](int a, int b) { return p[static_cast<std::size_t>(a)] > p[static_cast<std::size_t>(b)]; });
+    std::vector<char> keep(static_cast<std::size_t>(V), 0);
+    float cs = 0.f;
+    for (int id : idx) {
+      if (p[static_cast<std::size_t>(id)] <= 0.f) continue;
+      keep[static_cast<std::size_t>(id)] = 1;
+      cs += p[static_cast<std::size_t>(id)];
+      if (cs >= opts_.top_p) break;
+    }
+    float rn = 0.f;
+    for (int i = 0; i < V; ++i) {
+      if (!keep[static_cast<std::size_t>(i)]) p[static_cast<std::size_t>(i)] = 0.f;
+      rn += p[static_cast<std::size_t>(i)];
+    }
+    if (rn > 0.f) for (float& v : p) v /= rn;
+  }
+  std::uniform_real_distribution<float> dist(0.f, 1.f);
+  const float r = dist(rng_);
+  float acc = 0.f;
+  for (int i = 0; i < V; ++i) {
+    acc += p[static_cast<std::size_t>(i)];
+    if (r <= acc) return i;
+  }
+  return static_cast<int>(std::max_element(p.begin(), p.end()) - p.begin());
 }
 
 std::vector<float> LlamaEngine::next_logits(const std::vector<int>& prompt) {

@@ -10,6 +10,7 @@
 #include <cstddef>
 #include <cstdint>
 #include <functional>
+#include <random>
 #include <string>
 #include <utility>
 #include <vector>
@@ -156,7 +157,8 @@ class LlamaEngine {
   void* dmalloc(std::size_t bytes);
   uint16_t* upload_f16(const std::string& name, std::size_t expect_bytes);
 
-  void enqueue_step(bool with_head);
+  void enqueue_step(bool with_head, const cpi_sampling_params* sampling = nullptr);
+  void ensure_sample_graphs(const cpi_sampling_params& sp);
   void prefill_chunked(const std::vector<int>& prompt, int n_pre);
   void build_graphs();
   void run_graph(hipGraphExec_t g);
@@ -194,6 +196,18 @@ class LlamaEngine {
   int n_prompt_dev_ = 1;
 
   hipGraphExec_t g_decode_many_ = nullptr, g_decode_one_ = nullptr;
+  // sampled decoding on device (cpi_hip_sample_advance): graphs captured for
+  // the parameters in sample_params_; one uniform draw per token from rng_
+  // (mt19937(42), the generator of llama_engine_sampling_utils.cpp:173-175)
+  hipGraphExec_t g_sample_many_ = nullptr, g_sample_one_ = nullptr;
+  cpi_sampling_params sample_params_{};
+  bool device_sampling_ = false;  // vocab small enough for the device sampler
+  float* d_rand_ = nullptr;
+  uint32_t* d_seen_ = nullptr;    // bitmap of the ids in the history
+  int* d_hist_ = nullptr;         // the sequence so far, [0, *position]
+  int rand_len_ = 16;
+  std::vector<float> h_rand_;
+  std::mt19937 rng_{42};
   hipGraphExec_t g_prefill_many_ = nullptr, g_prefill_one_ = nullptr;
   int graph_steps_ = 16;
 

@@ -16,7 +16,7 @@ namespace {
 
 void usage(std::ostream& os) {
   os << "Usage: llama_infer <model.ll2c> --tokens csv [--max-new n] [--temp t] [--max-context n] "
-        "[--top-k n] [--top-p p] [--repeat-penalty r] [--rope-theta f] [--eos-token n] [--no-loop-guard] "
+        "[--top-k n] [--top-p p] [--repeat-penalty r] [--no-repeat-ngram n] [--rope-theta f] [--eos-token n] [--no-loop-guard] "
         "[--benchmark] [--benchmark-reps n] [--benchmark-warmup n] [--benchmark-phases] [--runtime-metrics] "
         "[--inspect-next-topk n] [--gpu-cache-all] [--no-resource-limits] [--graph-steps n] [--prefill-chunk n] [--quiet]\n";
 }
@@ -48,6 +48,8 @@ int main(int argc, char** argv) {
   opt.top_k = std::stoi(env_or("LLAMA_INFER_TOP_K", std::to_string(opt.top_k)));
   opt.top_p = std::stof(env_or("LLAMA_INFER_TOP_P", std::to_string(opt.top_p)));
   opt.eos_token_id = std::stoi(env_or("LLAMA_INFER_EOS_TOKEN_ID", std::to_string(opt.eos_token_id)));
+  opt.no_repeat_ngram_size =
+      std::stoi(env_or("LLAMA_INFER_NO_REPEAT_NGRAM", std::to_string(opt.no_repeat_ngram_size)));
 
   std::vector<int> tokens;
   int max_new = 16, reps = 1, warmup = 0, inspect_k = 0;
@@ -68,6 +70,7 @@ int main(int argc, char** argv) {
       else if (a == "--top-k") opt.top_k = std::stoi(next());
       else if (a == "--top-p") opt.top_p = std::stof(next());
       else if (a == "--repeat-penalty") opt.repetition_penalty = std::stof(next());
+      else if (a == "--no-repeat-ngram") opt.no_repeat_ngram_size = std::stoi(next());
       else if (a == "--rope-theta") opt.rope_theta = std::stof(next());
       else if (a == "--eos-token") opt.eos_token_id = std::stoi(next());
       else if (a == "--no-loop-guard") opt.loop_guard = false;

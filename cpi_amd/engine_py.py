@@ -17,7 +17,7 @@ class Options(ctypes.Structure):
                 ("eos_token_id", ctypes.c_int), ("loop_guard", ctypes.c_int), ("top_k", ctypes.c_int),
                 ("top_p", ctypes.c_float), ("repetition_penalty", ctypes.c_float), ("verbose", ctypes.c_int),
                 ("profile_decode_phases", ctypes.c_int), ("graph_steps", ctypes.c_int),
-                ("prefill_chunk", ctypes.c_int)]
+                ("prefill_chunk", ctypes.c_int), ("no_repeat_ngram_size", ctypes.c_int)]
 
 
 class Stats(ctypes.Structure):
@@ -59,13 +59,17 @@ def _ptr(a):
 
 class Engine:
     def __init__(self, path: str, max_context: int = 2048, eos: int = 2, loop_guard: bool = True,
-                 graph_steps: int = 16, verbose: bool = False, rope_theta: float = 0.0, prefill_chunk: int = 0):
+                 graph_steps: int = 16, verbose: bool = False, rope_theta: float = 0.0, prefill_chunk: int = 0,
+                 top_k: int = 40, top_p: float = 0.9, repetition_penalty: float = 1.0,
+                 no_repeat_ngram_size: int = 0):
         o = Options()
         lib().cpi_engine_default_options(ctypes.byref(o))
         self._path = path.encode()
         o.model_path, o.max_context, o.eos_token_id = self._path, max_context, eos
         o.loop_guard, o.graph_steps, o.verbose, o.rope_theta = int(loop_guard), graph_steps, int(verbose), rope_theta
         o.prefill_chunk = prefill_chunk
+        o.top_k, o.top_p, o.repetition_penalty = top_k, top_p, repetition_penalty
+        o.no_repeat_ngram_size = no_repeat_ngram_size
         self.h = lib().cpi_engine_create(ctypes.byref(o))
         if not self.h:
             raise RuntimeError(lib().cpi_engine_last_error().decode())

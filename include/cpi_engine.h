@@ -41,6 +41,7 @@ typedef struct cpi_engine_options {
                                GEMMs); 0 = LLAMA_INFER_PREFILL_CHUNK_SIZE or
                                128; 1 = token-by-token prefill
                                (llama_engine.cpp:1077-1078) */
+  int no_repeat_ngram_size; /* default 0 (off) */
 } cpi_engine_options;
 
 /* engine::BenchmarkStats (llama_engine.hpp:102-127), scalar fields. */

@@ -423,6 +423,31 @@ int cpi_hip_argmax_float(const float* logits, int n, int* out_index,
  * src/engine/llama_engine_graph.cpp:472-474. */
 int cpi_hip_greedy_advance(const float* logits, int n, int* token, int* position,
                            int* step, int* ring, int ring_len, cpi_stream_t stream);
+/* On-device sampling step, replacing the logits graph's host round trip
+ * (src/engine/llama_engine_graph.cpp:818-837: all V logits copied to the host
+ * per token) and the host sampler it feeds
+ * (src/engine/llama_engine_sampling_utils.cpp:10-189, sample_from_logits):
+ * sanitise/clamp, repetition penalty over the distinct history ids,
+ * no-repeat n-gram bans, temperature (<= 0: first max), top-k (values >= the
+ * k-th largest), softmax, top-p (most probable ids up to top_p, renormalised)
+ * and the inverse CDF at r = rand[*step % rand_len].  Then, like
+ * cpi_hip_greedy_advance: token = id, ring[*step % ring_len] = id, ++*step,
+ * ++*position; the id's bit is set in `seen` and history[*position] = id.
+ *   seen: device bitmap [ceil(vocab/32)] of the ids in the history (or null:
+ *         no repetition penalty); history: device int [history_cap] with the
+ *         sequence so far at [0, *position] (or null: no n-gram bans).
+ *   vocab <= 65536.  One workgroup; stream-ordered and graph-capturable. */
+typedef struct cpi_sampling_params {
+  float temperature;
+  int top_k;                 /* <= 0 or >= vocab: off */
+  float top_p;               /* outside (0, 1): off */
+  float repetition_penalty;  /* <= 1: off */
+  int no_repeat_ngram_size;  /* <= 1: off */
+} cpi_sampling_params;
+int cpi_hip_sample_advance(const float* logits, int vocab, const cpi_sampling_params* params,
+                           const float* rand, int rand_len, uint32_t* seen, int* history,
+                           int history_cap, int* token, int* position, int* step, int* ring,
+                           int ring_len, cpi_stream_t stream);
 /* Prompt step tail (sequential prefill inside a graph): ++*position, then
  * token = prompt[*position] when *position < n_prompt.  Replaces the host
  * token/position copies of the per-token prefill loop

@@ -44,6 +44,8 @@ def lib():
         L.oracle_router_topk.argtypes = [_p, _i, _i, _p, _p]
         L.oracle_argmax.restype = _i
         L.oracle_argmax.argtypes = [_p, _i]
+        L.oracle_sample.restype = _i
+        L.oracle_sample.argtypes = [_p, _i, _f, _i, _f, _f, _i, _p, _i, _f]
         L.oracle_engine_open.restype = _p
         L.oracle_engine_open.argtypes = [ctypes.c_char_p, _i, _f]
         L.oracle_engine_free.argtypes = [_p]
@@ -117,6 +119,15 @@ def router_topk(logits, top_k):
     prob = np.zeros(top_k, np.float32)
     lib().oracle_router_topk(_ptr(logits), logits.size, top_k, _ptr(idx), _ptr(prob))
     return idx, prob
+
+
+def sample(logits, temperature, top_k=0, top_p=1.0, rep_penalty=1.0, ngram=0, history=(), r=0.5):
+    """The resident engine's sampler (llama_engine_sampling_utils.cpp:10-189)
+    for one uniform draw r in [0, 1)."""
+    lg = np.array(logits, np.float32)
+    h = np.ascontiguousarray(np.asarray(history, np.int32))
+    return lib().oracle_sample(_ptr(lg), lg.size, temperature, top_k, top_p, rep_penalty, ngram,
+                               _ptr(h) if h.size else None, int(h.size), float(r))
 
 
 def argmax(x):

@@ -18,6 +18,7 @@
  *   MoE router + experts ...................... src/engine/cpu_engine.cpp:561-637
  *   forward_token ............................. src/engine/cpu_engine.cpp:650-706
  *   greedy (first max) ........................ src/engine/cpu_engine.cpp:726-729
+ *   sampling (GPU engine's sampler) ........... src/engine/llama_engine_sampling_utils.cpp:10-189
  *   generate_stream ........................... src/engine/cpu_engine.cpp:1064-1126
  *
  * Deliberate, documented deviations from the reference CPU engine:
@@ -301,6 +302,132 @@ EXPORT int oracle_argmax(const float* x, int n) {
   int best = 0;
   for (int i = 1; i < n; ++i) if (x[i] > x[best]) best = i;
   return best;
+}
+
+/* ----------------------------------------------------------- sampling
+ * The resident engine's sampler, src/engine/llama_engine_sampling_utils.cpp:
+ * 10-189 (sample_from_logits), in float as there, with the uniform draw r in
+ * [0, 1) passed in (the reference draws it from a thread-local mt19937(42)).
+ * Steps: non-finite -> -inf and clamp to [-80, 80] (:26-35); repetition
+ * penalty over the distinct history ids (:37-49); no-repeat n-gram bans
+ * (:55-94); temperature <= 0 -> first max (:96-98); scale by 1/T and max over
+ * finite (:100-113); top-k keeps values >= the k-th largest (:115-124);
+ * softmax (:126-139); top-p keeps the most probable ids until their sum
+ * reaches top_p, then renormalises (:141-171); first i with r <= cumulative
+ * probability, else the most probable id (:173-188).  Ties in the top-p
+ * order (unspecified under std::sort) are broken by lower id first.
+ * `logits` is modified.  Returns the sampled id. */
+static const float* g_sort_probs;
+static int cmp_prob_desc(const void* a, const void* b) {
+  const int i = *(const int*)a, j = *(const int*)b;
+  const float pi = g_sort_probs[i], pj = g_sort_probs[j];
+  if (pi > pj) return -1;
+  if (pi < pj) return 1;
+  return i < j ? -1 : (i > j);
+}
+static int cmp_float_desc(const void* a, const void* b) {
+  const float x = *(const float*)a, y = *(const float*)b;
+  return x > y ? -1 : (x < y);
+}
+
+EXPORT int oracle_sample(float* logits, int V, float temperature, int top_k, float top_p, float rep_penalty,
+                         int ngram, const int* history, int hist_len, float r) {
+  if (V <= 0) return 0;
+  for (int i = 0; i < V; ++i) {
+    float v = logits[i];
+    if (!isfinite(v)) { logits[i] = -INFINITY; continue; }
+    logits[i] = v > 80.f ? 80.f : (v < -80.f ? -80.f : v);
+  }
+  if (rep_penalty > 1.f && hist_len > 0) {
+    char* seen = (char*)calloc((size_t)V, 1);
+    for (int h = 0; h < hist_len; ++h) {
+      const int id = history[h];
+      if (id < 0 || id >= V || seen[id]) continue;
+      seen[id] = 1;
+      logits[id] = logits[id] > 0.f ? logits[id] / rep_penalty : logits[id] * rep_penalty;
+    }
+    free(seen);
+  }
+  if (ngram > 1 && hist_len + 1 >= ngram) {
+    const int pre = ngram - 1;
+    char* banned = (char*)calloc((size_t)V, 1);
+    for (int i = 0; i + ngram <= hist_len; ++i) {
+      int match = 1;
+      for (int j = 0; j < pre; ++j)
+        if (history[i + j] != history[hist_len - pre + j]) { match = 0; break; }
+      if (match) {
+        const int nx = history[i + pre];
+        if (nx >= 0 && nx < V) banned[nx] = 1;
+      }
+    }
+    int cand = 0;
+    for (int i = 0; i < V; ++i) {
+      if (banned[i]) logits[i] = -INFINITY;
+      else if (isfinite(logits[i])) cand = 1;
+    }
+    free(banned);
+    if (!cand) return 0;
+  }
+  if (temperature <= 0.f) {
+    int best = 0;
+    for (int i = 1; i < V; ++i) if (logits[i] > logits[best]) best = i;
+    return best;
+  }
+  const float inv_t = 1.f / temperature;
+  float mx = -INFINITY;
+  for (int i = 0; i < V; ++i)
+    if (isfinite(logits[i])) { const float s = logits[i] * inv_t; if (s > mx) mx = s; }
+  if (!isfinite(mx)) return 0;
+  for (int i = 0; i < V; ++i) logits[i] = logits[i] * inv_t;
+  if (top_k > 0 && top_k < V) {
+    float* copy = (float*)malloc(sizeof(float) * (size_t)V);
+    memcpy(copy, logits, sizeof(float) * (size_t)V);
+    qsort(copy, (size_t)V, sizeof(float), cmp_float_desc);
+    const float kth = copy[top_k - 1];
+    free(copy);
+    for (int i = 0; i < V; ++i) if (logits[i] < kth) logits[i] = -INFINITY;
+  }
+  float* p = (float*)calloc((size_t)V, sizeof(float));
+  float sum = 0.f;
+  for (int i = 0; i < V; ++i) {
+    if (!isfinite(logits[i])) continue;
+    p[i] = expf(logits[i] - mx);
+    sum += p[i];
+  }
+  if (sum <= 0.f) { free(p); return 0; }
+  for (int i = 0; i < V; ++i) p[i] /= sum;
+  if (top_p > 0.f && top_p < 1.f) {
+    int* idx = (int*)malloc(sizeof(int) * (size_t)V);
+    char* keep = (char*)calloc((size_t)V, 1);
+    for (int i = 0; i < V; ++i) idx[i] = i;
+    g_sort_probs = p;
+    qsort(idx, (size_t)V, sizeof(int), cmp_prob_desc);
+    float cs = 0.f;
+    for (int k = 0; k < V; ++k) {
+      const int id = idx[k];
+      if (p[id] <= 0.f) continue;
+      keep[id] = 1;
+      cs += p[id];
+      if (cs >= top_p) break;
+    }
+    float rn = 0.f;
+    for (int i = 0; i < V; ++i) { if (!keep[i]) p[i] = 0.f; rn += p[i]; }
+    if (rn > 0.f) for (int i = 0; i < V; ++i) p[i] /= rn;
+    free(idx);
+    free(keep);
+  }
+  float acc = 0.f;
+  int out = -1;
+  for (int i = 0; i < V; ++i) {
+    acc += p[i];
+    if (r <= acc) { out = i; break; }
+  }
+  if (out < 0) {
+    out = 0;
+    for (int i = 1; i < V; ++i) if (p[i] > p[out]) out = i;
+  }
+  free(p);
+  return out;
 }
 
 /* ------------------------------------------------------------- .ll2c file */

@@ -242,3 +242,73 @@ def test_converted_hf_checkpoint(tmp_path, quant):
     print(f"[engine] converted {quant}: max_abs_logit_err={err:.3e} identical_prefix={n}/32", flush=True)
     assert err <= LOGIT_TOL
     assert_ids_or_tie(n, rlg, err)
+
+
+def mt19937_float_draws(n, seed=42):
+    """The draws of std::mt19937(seed) through libstdc++'s
+    uniform_real_distribution<float>(0, 1): float(x) / 2^32 of each 32-bit
+    output, kept below 1."""
+    bg = np.random.MT19937()
+    bg._legacy_seeding(seed)
+    r = bg.random_raw(n).astype(np.float32) / np.float32(4294967296.0)
+    return np.minimum(r, np.nextafter(np.float32(1), np.float32(0))).astype(np.float32)
+
+
+SAMPLE_CASES = {
+    "T0.8_k40_p0.9": dict(temperature=0.8, top_k=40, top_p=0.9, rep=1.0, ngram=0),
+    "T1.0_rep1.2_ngram3": dict(temperature=1.0, top_k=0, top_p=1.0, rep=1.2, ngram=3),
+    "T0_rep1.3": dict(temperature=0.0, top_k=40, top_p=0.9, rep=1.3, ngram=0),
+}
+
+
+@pytest.mark.parametrize("name", list(SAMPLE_CASES))
+def test_sampled_decode_matches_oracle(tmp_path, name):
+    """Sampled decoding on device (cpi_hip_sample_advance inside the decode
+    graphs) against the oracle replaying the same model step by step and
+    sampling with the same draws (mt19937(42), one per token) and history
+    (prompt + generated ids)."""
+    from cpi_amd.engine_py import Engine
+    from tests.test_gpu_sampling import f64_probs
+    kw = SAMPLE_CASES[name]
+    print(f"[engine] sampled case={name}", flush=True)
+    cfg = tiny_cfg()
+    path = str(tmp_path / "s.ll2c")
+    ll2c.write_synthetic(path, ll2c.SynthSpec(cfg, attn_fmt="i4g32", mlp_fmt="i4g32", seed=5, std=0.02,
+                                              norm_jitter=0.1))
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab_size, 21)
+    n_new = 24
+    opts = dict(max_context=128, eos=-1, loop_guard=False, top_k=kw["top_k"], top_p=kw["top_p"],
+                repetition_penalty=kw["rep"], no_repeat_ngram_size=kw["ngram"])
+    eng = Engine(path, **opts)
+    ids, lg = eng.generate(prompt, n_new, temperature=kw["temperature"], logit_steps=n_new)
+    eng.close()
+    eng2 = Engine(path, **opts)  # fresh draw stream; batched (16-step) graphs
+    ids2, _ = eng2.generate(prompt, n_new, temperature=kw["temperature"])
+    eng2.close()
+    assert (ids2 == ids).all()
+
+    o = oracle.Engine(path, 128)
+    for p, t in enumerate(prompt[:-1]):
+        o.forward(int(t), p)
+    draws = mt19937_float_draws(n_new)
+    hist, cur, pos = [int(t) for t in prompt], int(prompt[-1]), len(prompt) - 1
+    agree = 0
+    for i in range(n_new):
+        lo = o.forward(cur, pos)
+        err = np.abs(lg[i] - lo).max()
+        assert err <= LOGIT_TOL, i
+        nxt = oracle.sample(lo, kw["temperature"], kw["top_k"], kw["top_p"], kw["rep"], kw["ngram"], hist, draws[i])
+        if nxt != ids[i]:
+            # a logit error e moves every cumulative boundary by at most about
+            # 2 e / T: only a draw that close to one may split the two
+            p = f64_probs(lo, max(kw["temperature"], 1e-6), kw["top_k"], kw["top_p"], kw["rep"], kw["ngram"], hist)
+            margin = np.min(np.abs(np.cumsum(p) - draws[i]))
+            bound = 4 * err / max(kw["temperature"], 1e-6) + 1e-5
+            print(f"[engine] split at step {i}: oracle {nxt} engine {int(ids[i])} draw {draws[i]:.6f} "
+                  f"margin {margin:.2e} bound {bound:.2e} err {err:.2e}", flush=True)
+            assert kw["temperature"] > 0 and margin < bound, (i, nxt, int(ids[i]), margin, bound)
+            break
+        agree += 1
+        hist.append(nxt)
+        cur, pos = nxt, pos + 1
+    print(f"[engine] sampled {name}: {agree}/{n_new} ids identical to the oracle", flush=True)

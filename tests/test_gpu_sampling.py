@@ -1,0 +1,152 @@
+"""GPU parity of the on-device sampler (cpi_hip_sample_advance) with the
+oracle's restatement of the engine sampler (llama_engine_sampling_utils.cpp:
+10-189).  Draws r are taken at least 1e-5 away from every cumulative
+boundary of a float64 restatement, so the float summation order (blocked on
+the GPU, sequential in the reference) cannot decide the pick; the picks must
+then be identical."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from cpi_amd import _lib
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    from tests import gpu_util as G
+
+
+def f64_probs(lg, temperature, top_k=0, top_p=1.0, rep=1.0, ngram=0, history=()):
+    """Float64 restatement (for choosing draws away from boundaries only)."""
+    x = np.array(lg, np.float64)
+    x = np.where(np.isfinite(x), np.clip(x, -80, 80), -np.inf)
+    if rep > 1:
+        for i in set(int(h) for h in history):
+            x[i] = x[i] / rep if x[i] > 0 else x[i] * rep
+    if ngram > 1 and len(history) + 1 >= ngram:
+        h, pre = list(history), ngram - 1
+        for i in range(len(h) - ngram + 1):
+            if h[i:i + pre] == h[len(h) - pre:]:
+                x[h[i + pre]] = -np.inf
+    s = x / temperature
+    if 0 < top_k < s.size:
+        s[s < np.sort(s)[::-1][top_k - 1]] = -np.inf
+    p = np.where(np.isfinite(s), np.exp(s - s[np.isfinite(s)].max()), 0.0)
+    p /= p.sum()
+    if 0 < top_p < 1:
+        order = np.lexsort((np.arange(p.size), -p))
+        m = int(np.searchsorted(np.cumsum(p[order]), top_p) + 1)
+        keep = np.zeros(p.size, bool)
+        keep[order[:m]] = True
+        p = np.where(keep, p, 0.0)
+        p /= p.sum()
+    return p
+
+
+def safe_draws(p, n, rng):
+    cum = np.cumsum(p)
+    out = []
+    while len(out) < n:
+        r = float(np.float32(rng.random()))
+        if np.min(np.abs(cum - r)) > 1e-5:
+            out.append(r)
+    return out
+
+
+def run(lg, params, r, history=None, pos=None, seen=True):
+    """One sample_advance on device; returns (id, token, position, step, ring,
+    seen words, history)."""
+    V = lg.size
+    d_lg = G.dev(lg.astype(np.float32))
+    d_r = G.dev(np.array([0.0, r, 0.0], np.float32))
+    hist = np.zeros(256, np.int32)
+    if history is not None:
+        hist[:len(history)] = history
+    position = (len(history) - 1) if history is not None else (pos or 0)
+    bits = np.zeros((V + 31) // 32, np.uint32)
+    if history is not None and seen:
+        for h in set(history):
+            bits[h >> 5] |= np.uint32(1 << (h & 31))
+    d_bits, d_hist = G.dev(bits), G.dev(hist)
+    state = G.dev(np.array([0, position, 1], np.int32))  # token, position, step
+    ring = G.dev(np.full(4, -1, np.int32))
+    base = state.data_ptr()
+    _lib.call("cpi_hip_sample_advance", G.ptr(d_lg), V, ctypes.byref(params), G.ptr(d_r), 3,
+              G.ptr(d_bits) if seen else None, G.ptr(d_hist) if history is not None else None, 256,
+              ctypes.c_void_p(base), ctypes.c_void_p(base + 4), ctypes.c_void_p(base + 8), G.ptr(ring), 4,
+              G.stream())
+    tok, p2, st = G.host(state, np.int32, 3)
+    return int(tok), int(p2), int(st), G.host(ring, np.int32, 4), G.host(d_bits, np.uint32), G.host(d_hist, np.int32)
+
+
+CASES = {
+    "softmax_T0.8": dict(temperature=0.8),
+    "topk40": dict(temperature=1.0, top_k=40),
+    "topp0.9": dict(temperature=0.7, top_p=0.9),
+    "topk50_topp0.95_rep1.3": dict(temperature=1.1, top_k=50, top_p=0.95, rep=1.3),
+    "ngram3_T0.9": dict(temperature=0.9, ngram=3),
+}
+
+
+@pytest.mark.parametrize("V", [32000, 50000, 1000])
+@pytest.mark.parametrize("case", list(CASES))
+def test_sample_matches_oracle(case, V):
+    print(f"[sample] case={case} V={V}", flush=True)
+    kw = CASES[case]
+    rng = np.random.default_rng(V + len(case))
+    lg = (rng.standard_normal(V) * 3).astype(np.float32)
+    lg[rng.integers(0, V, 3)] = [np.nan, np.inf, -np.inf]
+    hist = list(rng.integers(0, V, 40))
+    hist += hist[5:8] + hist[5:7]  # a repeated trigram prefix for the n-gram case
+    params = _lib.SamplingParams(kw["temperature"], kw.get("top_k", 0), kw.get("top_p", 1.0), kw.get("rep", 1.0),
+                                 kw.get("ngram", 0))
+    p = f64_probs(lg, kw["temperature"], kw.get("top_k", 0), kw.get("top_p", 1.0), kw.get("rep", 1.0),
+                  kw.get("ngram", 0), hist)
+    for r in safe_draws(p, 6, rng):
+        want = oracle.sample(lg, kw["temperature"], kw.get("top_k", 0), kw.get("top_p", 1.0), kw.get("rep", 1.0),
+                             kw.get("ngram", 0), hist, r)
+        got, pos, step, ring, bits, h = run(lg, params, r, history=hist)
+        assert got == want, (r, got, want)
+        assert p[got] > 0
+        assert pos == len(hist) and step == 2 and ring[1] == got and h[len(hist)] == got
+        assert (bits[got >> 5] >> (got & 31)) & 1
+
+
+def test_sample_greedy_with_penalty_and_ngram():
+    """temperature 0 with a repetition penalty or n-gram bans: first maximum
+    after them (the engine routes these through the sampler)."""
+    V = 4096
+    lg = np.zeros(V, np.float32)
+    lg[[10, 20, 30]] = [5.0, 4.9, 4.0]
+    hist = [1, 10, 2, 1]  # 10 followed "1" before; the suffix is "1"
+    for params, want in [(_lib.SamplingParams(0.0, 0, 1.0, 1.2, 0), 20),   # 5/1.2 < 4.9
+                         (_lib.SamplingParams(0.0, 0, 1.0, 1.0, 2), 20),   # 10 banned after "1"
+                         (_lib.SamplingParams(0.0, 0, 1.0, 1.0, 0), 10)]:
+        got = run(lg, params, 0.5, history=hist)[0]
+        assert got == want == oracle.sample(lg, 0.0, 0, 1.0, params.repetition_penalty,
+                                            params.no_repeat_ngram_size, hist, 0.5)
+
+
+def test_sample_ties_at_topk_and_all_masked():
+    V = 2048
+    lg = np.full(V, -5.0, np.float32)
+    lg[[3, 700, 1500]] = 2.0
+    params = _lib.SamplingParams(1.0, 2, 1.0, 1.0, 0)  # k = 2 keeps all three tied values
+    picks = {run(lg, params, (j + 0.5) / 12)[0] for j in range(12)}
+    assert picks == {3, 700, 1500}
+    nan = np.full(V, np.nan, np.float32)  # nothing finite: id 0, as the reference
+    assert run(nan, _lib.SamplingParams(1.0, 0, 1.0, 1.0, 0), 0.3)[0] == 0
+
+
+def test_sample_rejects_bad_args():
+    x = G.empty(1024)
+    p = _lib.SamplingParams(1.0, 0, 1.0, 1.0, 0)
+    L = _lib.lib()
+    args = [G.ptr(x), 1 << 17, ctypes.byref(p), G.ptr(x), 1, None, None, 0, G.ptr(x), G.ptr(x), G.ptr(x), G.ptr(x),
+            1, G.stream()]
+    assert L.cpi_hip_sample_advance(*args) == -1  # vocab too large
+    args[1], args[4] = 100, 0
+    assert L.cpi_hip_sample_advance(*args) == -1  # rand_len

@@ -163,3 +163,51 @@ def test_engine_vs_float64_decoder(tmp_path, attn, mlp, extra):
     scale = np.abs(rlg).max()
     np.testing.assert_allclose(lg, rlg, atol=2e-5 * max(scale, 1))
     assert (ids == rids).all()
+
+
+def test_sampler_closed_forms():
+    """oracle.sample (llama_engine_sampling_utils.cpp:10-189) against what the
+    mathematics fixes: greedy limits, uniform logits, the softmax distribution
+    over a grid of draws, distinct-id repetition penalty, n-gram bans, ties at
+    the top-k threshold."""
+    rng = np.random.default_rng(11)
+    lg = rng.standard_normal(500).astype(np.float32) * 2
+    am = int(np.argmax(lg))
+    assert oracle.sample(lg, 0.0) == am
+    assert oracle.sample(lg, 0.7, top_k=1, r=0.999) == am
+    assert oracle.sample(lg, 1.3, top_p=1e-6, r=0.999) == am
+    # uniform logits: first i with r <= (i + 1) / V
+    V = 1000
+    for r in (0.0004, 0.2503, 0.77777, 0.9995):
+        assert oracle.sample(np.zeros(V, np.float32), 1.0, r=r) == int(np.ceil(r * V)) - 1
+    # inverse-CDF over a grid of N draws reproduces N * softmax to within one draw per id
+    small = rng.standard_normal(12).astype(np.float32)
+    T, N = 0.8, 4000
+    p = np.exp((small.astype(np.float64) - small.max()) / T)
+    p /= p.sum()
+    counts = np.bincount([oracle.sample(small, T, r=(j + 0.5) / N) for j in range(N)], minlength=12)
+    assert np.all(np.abs(counts - N * p) <= 1.5)
+    # top-k: only the k largest can be drawn; top-p: only the smallest prefix reaching p
+    picks = {oracle.sample(small, T, top_k=3, r=(j + 0.5) / 200) for j in range(200)}
+    assert picks == set(np.argsort(-small)[:3].tolist())
+    order = np.argsort(-p)
+    m = int(np.searchsorted(np.cumsum(p[order]), 0.6) + 1)
+    picks = {oracle.sample(small, T, top_p=0.6, r=(j + 0.5) / 200) for j in range(200)}
+    assert picks == set(order[:m].tolist())
+    # repetition penalty: once per distinct id, divide positives, multiply negatives
+    base = np.array([2.0, -1.0, 1.5, 0.5], np.float32)
+    for hist in ([0, 0, 0, 1], [0, 1]):
+        want = base.copy()
+        want[0] /= 1.5
+        want[1] *= 1.5
+        assert oracle.sample(base, 0.0, rep_penalty=1.5, history=hist) == int(np.argmax(want)) == 2
+    # n-gram 2: after "... 7" every id that followed a 7 is banned
+    hist = [7, 3, 5, 7, 9, 7]
+    lg2 = np.zeros(12, np.float32)
+    lg2[[3, 9]] = 5.0
+    lg2[4] = 4.0
+    assert oracle.sample(lg2, 0.0, ngram=2, history=hist) == 4
+    assert all(oracle.sample(lg2, 1.0, ngram=2, history=hist, r=(j + 0.5) / 50) not in (3, 9) for j in range(50))
+    # ties at the k-th value are all kept (values below it are not)
+    tie = np.array([1.0, 3.0, 2.0, 3.0, 3.0], np.float32)
+    assert {oracle.sample(tie, 1.0, top_k=2, r=(j + 0.5) / 30) for j in range(30)} == {1, 3, 4}
