@@ -50,7 +50,7 @@ class SamplingParams(ctypes.Structure):
                 ("repetition_penalty", ctypes.c_float), ("no_repeat_ngram_size", c_int)]
 
 
-W_F16, W_I8ROW, W_I4ROW, W_I4G32 = 0, 1, 2, 3
+W_F16, W_I8ROW, W_I4ROW, W_I4G32, W_I4G32B = 0, 1, 2, 3, 4
 EPI_STORE_F32, EPI_STORE_F16, EPI_RESID_ADD, EPI_SWIGLU, EPI_QKV_ROPE, EPI_SWIGLU_F16 = 0, 1, 2, 3, 4, 5
 ATTN_MAX_SPLITS = 256
 PREFILL_COUNTER_BYTES = 16384
@@ -70,6 +70,8 @@ _SIGS = {
     "cpi_hip_qkv_row_order": (c_int, [c_int, c_int, c_int, c_int_p]),
     "cpi_hip_swiglu_row_order": (c_int, [c_int, c_int_p]),
     "cpi_hip_gather_rows": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_size_t, c_void_p]),
+    "cpi_hip_blocked_scale_count": (c_size_t, [c_int, c_int]),
+    "cpi_hip_block_group_scales": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "cpi_hip_attention_scratch_floats": (c_size_t, [c_int, c_int]),
     "cpi_hip_attention_decode": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int,
                                          c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),

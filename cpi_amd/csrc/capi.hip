@@ -51,6 +51,8 @@ int gemv_common(int wfmt, int epi, const void* w, const void* scales, int scale_
   if (((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15) != 0)
     return fail(std::string(who) + ": weights and x must be 16-byte aligned");
   if (wfmt != CPI_W_F16 && !scales) return fail(std::string(who) + ": missing scales");
+  if (wfmt == CPI_W_I4G32B && (reinterpret_cast<uintptr_t>(scales) & 15) != 0)
+    return fail(std::string(who) + ": blocked scales must be 16-byte aligned");
   cpi::GemvParams p{};
   p.w = w;
   p.scales = scales;
@@ -127,6 +129,8 @@ static int gemv_params(const cpi_gemv_desc* d, cpi::GemvParams& p) {
         reinterpret_cast<uintptr_t>(d->norm_w)) & 15) != 0)
     return fail("gemv: weights, x and norm_w must be 16-byte aligned");
   if (d->wfmt != CPI_W_F16 && !d->scales) return fail("gemv: missing scales");
+  if (d->wfmt == CPI_W_I4G32B && (reinterpret_cast<uintptr_t>(d->scales) & 15) != 0)
+    return fail("gemv: blocked scales must be 16-byte aligned");
   if (d->wfmt == CPI_W_I8ROW || d->wfmt == CPI_W_I4ROW) {
     if (d->scale_count != 1 && d->scale_count != d->out_features)
       return fail("gemv: scale_count must be 1 or out_features");
@@ -238,6 +242,18 @@ int cpi_hip_gather_rows(const void* src, void* dst, const int* idx, int rows, si
                      static_cast<const uint8_t*>(src), static_cast<uint8_t*>(dst), idx, rows,
                      row_bytes);
   return check(hipGetLastError(), "gather_rows");
+}
+
+size_t cpi_hip_blocked_scale_count(int rows, int groups) {
+  return rows > 0 && groups > 0 ? cpi::blocked_scale_elems(rows, groups) : 0;
+}
+
+int cpi_hip_block_group_scales(const uint16_t* src, uint16_t* dst, int rows, int groups, cpi_stream_t s) {
+  if (!src || !dst || rows <= 0 || groups <= 0) return fail("block_group_scales: bad arguments");
+  const size_t n = cpi::blocked_scale_elems(rows, groups);
+  const int grid = static_cast<int>(std::min<size_t>((n + 255) / 256, 4096));
+  hipLaunchKernelGGL(cpi::block_group_scales_kernel, dim3(grid), dim3(256), 0, S(s), src, dst, rows, groups);
+  return check(hipGetLastError(), "block_group_scales");
 }
 
 // ------------------------------------------------------------ attention

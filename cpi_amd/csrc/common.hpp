@@ -5,7 +5,13 @@
 #include <cstdint>
 #include <cstddef>
 
+#include "../../include/cpi_hip.h"
+
 namespace cpi {
+
+// Weight formats with one fp16 scale per 32-value group (row-major or blocked).
+template <int FMT>
+constexpr bool kGroupScaled = FMT == CPI_W_I4G32 || FMT == CPI_W_I4G32B;
 
 typedef _Float16 f16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));

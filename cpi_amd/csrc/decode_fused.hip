@@ -78,7 +78,7 @@ using CfgLM = TileCfg<4, 4, 2>;   // 8 rows x K <= 4096 (fp16)
 // Weight loads of one tile held in registers (16-byte chunks + group scales).
 struct WBuf {
   u32x4 w[kMaxLoads];
-  uint16_t s[kMaxLoads];
+  uint32_t s[kMaxLoads];  // GroupScales words of pass q at [q * nr, (q + 1) * nr)
 };
 
 // ---------------------------------------------------------------------------
@@ -128,10 +128,15 @@ __device__ __forceinline__ void tile_issue(const uint8_t* W, const uint16_t* S, 
   for (int q = 0; q < C::pp; ++q) {
     const int pass = clamp_pass(g, sg, plan_pass(g, sg, 0, q));
     const int c = clamp_chunk(g, pass, lane);
+    if constexpr (kGroupScaled<FMT>) {
+      GroupScales<FMT, C::nr> gs;
+      gs.load(S, g, plan_row(g, tile, rs, 0), c);
+#pragma unroll
+      for (int j = 0; j < static_cast<int>(sizeof(gs.w) / 4); ++j) b.s[q * C::nr + j] = gs.w[j];
+    }
 #pragma unroll
     for (int i = 0; i < C::nr; ++i) {
       const int row = clamp_row(g, plan_row(g, tile, rs, i));
-      if constexpr (FMT == CPI_W_I4G32) b.s[i * C::pp + q] = S[scale_index(g, row, c)];
       b.w[i * C::pp + q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W + weight_offset(g, row, c)));
     }
   }
@@ -158,11 +163,14 @@ __device__ __forceinline__ void tile_compute(int R, int K, int tile, const WBuf&
     if (c < g.nchunks) {
       XPrep<FMT> xp;
       read_prep<FMT>(prep + c * F::kStride, xp);
-      if constexpr (FMT == CPI_W_I4G32) {
+      if constexpr (kGroupScaled<FMT>) {
         const float bias = chunk_bias<FMT>(xp);
+        GroupScales<FMT, C::nr> gs;
+#pragma unroll
+        for (int j = 0; j < static_cast<int>(sizeof(gs.w) / 4); ++j) gs.w[j] = b.s[q * C::nr + j];
 #pragma unroll
         for (int i = 0; i < C::nr; ++i)
-          acc[i] = fmaf(h2f(b.s[i * C::pp + q]), chunk_dot<FMT>(b.w[i * C::pp + q], xp, bias), acc[i]);
+          acc[i] = fmaf(gs.scale(i), chunk_dot<FMT>(b.w[i * C::pp + q], xp, bias), acc[i]);
       } else {
 #pragma unroll
         for (int i = 0; i < C::nr; ++i) acc[i] = chunk_dot<FMT>(b.w[i * C::pp + q], xp, acc[i]);
@@ -362,7 +370,7 @@ __device__ __forceinline__ void prefetch_first(const uint8_t* W, const uint16_t*
 // ---------------------------------------------------------------------------
 // The kernel.
 // ---------------------------------------------------------------------------
-constexpr int kFusedPrepWords = (12288 / 32) * FmtT<CPI_W_I4G32>::kStride;  // largest prepared vector
+constexpr int kFusedPrepWords = (12288 / 32) * FmtT<CPI_W_I4G32B>::kStride;  // largest prepared vector
 static_assert(kFusedPrepWords >= (4096 / 8) * FmtT<CPI_W_F16>::kStride, "lm_head prep fits");
 
 template <int HD, int GQ>
@@ -390,7 +398,7 @@ __global__ void __launch_bounds__(kBlock, 2) decode_fused_kernel(FusedParams P) 
   barrier_arrive(P, target, live);
   {
     const cpi_fused_layer& L0 = P.layers[0];
-    prefetch_first<CPI_W_I4G32, CfgQKV>(static_cast<const uint8_t*>(L0.wqkv), static_cast<const uint16_t*>(L0.sqkv),
+    prefetch_first<CPI_W_I4G32B, CfgQKV>(static_cast<const uint8_t*>(L0.wqkv), static_cast<const uint16_t*>(L0.sqkv),
                                         qkv_rows, H, wb);
   }
   barrier_wait(P, target, live);
@@ -410,7 +418,7 @@ __global__ void __launch_bounds__(kBlock, 2) decode_fused_kernel(FusedParams P) 
   for (int l = 0; l < P.nlayers; ++l) {
     const cpi_fused_layer& L = P.layers[l];
     // QKV + RMSNorm + RoPE + KV store
-    gemv_phase<CPI_W_I4G32, CfgQKV, FE_QKV, true>(P, L, static_cast<const uint8_t*>(L.wqkv),
+    gemv_phase<CPI_W_I4G32B, CfgQKV, FE_QKV, true>(P, L, static_cast<const uint8_t*>(L.wqkv),
                                                   static_cast<const uint16_t*>(L.sqkv), qkv_rows, H, P.x,
                                                   L.norm_att, pos, wb, prep, part, fin, red, best);
     barrier_arrive(P, target, live);
@@ -423,33 +431,33 @@ __global__ void __launch_bounds__(kBlock, 2) decode_fused_kernel(FusedParams P) 
       attn_body<HD, GQ, true, true, true>(ap, it % P.nkv, it / P.nkv);
     }
     barrier_arrive(P, target, live);
-    prefetch_first<CPI_W_I4G32, CfgO>(static_cast<const uint8_t*>(L.wo), static_cast<const uint16_t*>(L.so), H, qdim,
+    prefetch_first<CPI_W_I4G32B, CfgO>(static_cast<const uint8_t*>(L.wo), static_cast<const uint16_t*>(L.so), H, qdim,
                                       wb);
     barrier_wait(P, target, live);
     // o_proj + residual
-    gemv_phase<CPI_W_I4G32, CfgO, FE_RESID, false>(P, L, static_cast<const uint8_t*>(L.wo),
+    gemv_phase<CPI_W_I4G32B, CfgO, FE_RESID, false>(P, L, static_cast<const uint8_t*>(L.wo),
                                                    static_cast<const uint16_t*>(L.so), H, qdim, P.att, nullptr, pos,
                                                    wb, prep, part, fin, red, best);
     barrier_arrive(P, target, live);
-    prefetch_first<CPI_W_I4G32, CfgW13>(static_cast<const uint8_t*>(L.w13), static_cast<const uint16_t*>(L.s13),
+    prefetch_first<CPI_W_I4G32B, CfgW13>(static_cast<const uint8_t*>(L.w13), static_cast<const uint16_t*>(L.s13),
                                         2 * I, H, wb);
     barrier_wait(P, target, live);
     // w1|w3 + RMSNorm + SwiGLU
-    gemv_phase<CPI_W_I4G32, CfgW13, FE_SWIGLU, true>(P, L, static_cast<const uint8_t*>(L.w13),
+    gemv_phase<CPI_W_I4G32B, CfgW13, FE_SWIGLU, true>(P, L, static_cast<const uint8_t*>(L.w13),
                                                      static_cast<const uint16_t*>(L.s13), 2 * I, H, P.x,
                                                      L.norm_ffn, pos, wb, prep, part, fin, red, best);
     barrier_arrive(P, target, live);
-    prefetch_first<CPI_W_I4G32, CfgW2>(static_cast<const uint8_t*>(L.w2), static_cast<const uint16_t*>(L.s2), H, I,
+    prefetch_first<CPI_W_I4G32B, CfgW2>(static_cast<const uint8_t*>(L.w2), static_cast<const uint16_t*>(L.s2), H, I,
                                        wb);
     barrier_wait(P, target, live);
     // w2 + residual
-    gemv_phase<CPI_W_I4G32, CfgW2, FE_RESID, false>(P, L, static_cast<const uint8_t*>(L.w2),
+    gemv_phase<CPI_W_I4G32B, CfgW2, FE_RESID, false>(P, L, static_cast<const uint8_t*>(L.w2),
                                                     static_cast<const uint16_t*>(L.s2), H, I, P.ff, nullptr, pos,
                                                     wb, prep, part, fin, red, best);
     barrier_arrive(P, target, live);
     if (l + 1 < P.nlayers) {
       const cpi_fused_layer& N = P.layers[l + 1];
-      prefetch_first<CPI_W_I4G32, CfgQKV>(static_cast<const uint8_t*>(N.wqkv), static_cast<const uint16_t*>(N.sqkv),
+      prefetch_first<CPI_W_I4G32B, CfgQKV>(static_cast<const uint8_t*>(N.wqkv), static_cast<const uint16_t*>(N.sqkv),
                                           qkv_rows, H, wb);
     } else {
       prefetch_first<CPI_W_F16, CfgLM>(reinterpret_cast<const uint8_t*>(P.lm_w), nullptr, P.V, H, wb);
@@ -513,13 +521,13 @@ bool fused_supported(const cpi_fused_decode_desc& d, const char** why) {
   if (G != 1 && G != 2 && G != 4 && G != 8) return no("GQA group must be 1, 2, 4 or 8");
   const int qdim = d.num_heads * d.head_dim;
   if (d.hidden % 32 || d.intermediate % 32 || qdim % 32) return no("dims must be multiples of 32");
-  if (np_of<CPI_W_I4G32>(d.hidden) > CfgQKV::pp * CfgQKV::ks || np_of<CPI_W_I4G32>(d.hidden) > CfgW13::pp * CfgW13::ks)
+  if (np_of<CPI_W_I4G32B>(d.hidden) > CfgQKV::pp * CfgQKV::ks || np_of<CPI_W_I4G32B>(d.hidden) > CfgW13::pp * CfgW13::ks)
     return no("hidden too large for the fused tiles");
-  if (np_of<CPI_W_I4G32>(qdim) > CfgO::pp * CfgO::ks) return no("q dim too large for the fused tiles");
-  if (np_of<CPI_W_I4G32>(d.intermediate) > CfgW2::pp * CfgW2::ks) return no("intermediate too large");
+  if (np_of<CPI_W_I4G32B>(qdim) > CfgO::pp * CfgO::ks) return no("q dim too large for the fused tiles");
+  if (np_of<CPI_W_I4G32B>(d.intermediate) > CfgW2::pp * CfgW2::ks) return no("intermediate too large");
   if (np_of<CPI_W_F16>(d.hidden) > CfgLM::pp * CfgLM::ks) return no("hidden too large for the lm_head tiles");
   if (d.hidden > 4096) return no("hidden > 4096");
-  if (d.intermediate / 32 * FmtT<CPI_W_I4G32>::kStride > kFusedPrepWords) return no("intermediate too large");
+  if (d.intermediate / 32 * FmtT<CPI_W_I4G32B>::kStride > kFusedPrepWords) return no("intermediate too large");
   if (d.intermediate % 4 != 0) return no("intermediate % 4");
   return true;
 }

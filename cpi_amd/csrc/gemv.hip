@@ -55,6 +55,41 @@ template <> struct FmtT<CPI_W_I4ROW> {
   static constexpr int kStride = 20;  // 16 pair dwords + -C, padded to 16 B
 };
 template <> struct FmtT<CPI_W_I4G32> : FmtT<CPI_W_I4ROW> {};
+template <> struct FmtT<CPI_W_I4G32B> : FmtT<CPI_W_I4ROW> {};
+
+// Group scales of the NR consecutive rows row0 .. row0+NR-1 (row0 a multiple
+// of NR) at chunk c (clamped), kept as loaded: NR zero-extended 2-byte loads
+// from the row-major layout, or one NR * 2-byte load from the blocked layout
+// (packed pairs).  The halves are taken at use (scale()), so nothing waits for
+// the load while the weight loads behind it are being issued.
+template <int FMT, int NR>
+struct GroupScales {
+  static constexpr bool kBlocked = FMT == CPI_W_I4G32B;
+  uint32_t w[kBlocked ? (NR + 1) / 2 : NR];
+
+  __device__ __forceinline__ void load(const uint16_t* S, const GemvPlan& g, int row0, int c) {
+    if constexpr (kBlocked) {
+      static_assert(NR == 8 || NR == 4 || NR == 2, "blocked scales: 2, 4 or 8 rows per wave");
+      const uint16_t* src = S + scale_block_index(g, clamp_row_group(g, row0, NR), c);
+      if constexpr (NR == 8) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(src);
+        w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+      } else if constexpr (NR == 4) {
+        const uint2 v = *reinterpret_cast<const uint2*>(src);
+        w[0] = v.x; w[1] = v.y;
+      } else {
+        w[0] = *reinterpret_cast<const uint32_t*>(src);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NR; ++i) w[i] = S[scale_index(g, clamp_row(g, row0 + i), c)];
+    }
+  }
+  __device__ __forceinline__ float scale(int i) const {
+    if constexpr (kBlocked) return static_cast<float>((i & 1) ? as_h2(w[i >> 1]).y : as_h2(w[i >> 1]).x);
+    else return static_cast<float>(as_h2(w[i]).x);
+  }
+};
 
 struct GemvParams {
   const void* w;
@@ -224,7 +259,7 @@ __device__ __forceinline__ float prep_unit(const float* v, uint32_t* dst, int d)
 template <int FMT>
 __device__ __forceinline__ void store_bias(uint32_t* dst, float s) {
   if constexpr (FMT == CPI_W_I8ROW) dst[8] = __builtin_bit_cast(uint32_t, -1152.f * s);
-  else if constexpr (FMT == CPI_W_I4ROW || FMT == CPI_W_I4G32) dst[16] = __builtin_bit_cast(uint32_t, -s);
+  else if constexpr (FMT == CPI_W_I4ROW || kGroupScaled<FMT>) dst[16] = __builtin_bit_cast(uint32_t, -s);
 }
 
 // Per-lane select by a constant lane pattern (bit l of `mask` picks `a` in lane l).
@@ -429,7 +464,10 @@ __device__ __forceinline__ void row_epilogue(const GemvParams& p, int epi, int r
 // segments.  Per group a wave issues NR x PP 16-byte loads per lane (clamped
 // in-bounds addresses), then consumes them pass by pass.
 // ---------------------------------------------------------------------------
-template <int FMT, bool XF32, int NR, int PP, int MAXU, bool FOLD, bool GATHER>
+// DB: double-buffered groups (a wave issues group k + 1 before it computes
+// group k), for plans with several groups per wave (long K); the groups are
+// still accumulated in order, so results equal the single-buffered kernel's.
+template <int FMT, bool XF32, int NR, int PP, int MAXU, bool FOLD, bool GATHER, bool DB>
 __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int epi, int ks) {
   static_assert(!FOLD || (XF32 && MAXU <= 2), "the folded residual update needs fp32 x held in registers");
   if constexpr (GATHER) {
@@ -498,22 +536,25 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int epi, int
 
   // ---- group-0 weight loads: issued behind the activation loads, so waiting
   // for the activations (vmcnt = number of weight loads) leaves them in flight
-  u32x4 wv[NR][PP];
-  uint16_t gsc[NR][PP];
-  auto issue = [&](int grp) {
+  struct Group {
+    u32x4 wv[NR][PP];
+    GroupScales<FMT, NR> gsc[PP];
+  };
+  Group ga, gb;
+  auto issue = [&](int grp, Group& b) {
 #pragma unroll
     for (int q = 0; q < PP; ++q) {
       const int pass = clamp_pass(g, sg, plan_pass(g, sg, grp, q));
       const int c = clamp_chunk(g, pass, lane);
+      if constexpr (kGroupScaled<FMT>) b.gsc[q].load(G, g, plan_row(g, block, rs, 0), c);
 #pragma unroll
       for (int i = 0; i < NR; ++i) {
         const int row = clamp_row(g, plan_row(g, block, rs, i));
-        if constexpr (FMT == CPI_W_I4G32) gsc[i][q] = G[scale_index(g, row, c)];
-        wv[i][q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W + weight_offset(g, row, c)));
+        b.wv[i][q] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(W + weight_offset(g, row, c)));
       }
     }
   };
-  issue(0);
+  issue(0, ga);
 
   // ---- RMSNorm statistics and activation preparation into LDS
   if (in_regs) {
@@ -647,7 +688,7 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int epi, int
 #pragma unroll
   for (int i = 0; i < NR; ++i) acc[i] = 0.f;
   float bias_sum = 0.f;  // per-row-scale formats: bias constants, shared by all rows
-  auto compute = [&](int grp) {
+  auto compute = [&](int grp, const Group& b) {
 #pragma unroll
     for (int q = 0; q < PP; ++q) {
       const int pass = plan_pass(g, sg, grp, q);
@@ -656,22 +697,41 @@ __global__ void __launch_bounds__(kBlock) gemv_kernel(GemvParams p, int epi, int
       if (c < nchunks) {
         XPrep<FMT> xp;
         read_prep<FMT>(lds + c * F::kStride, xp);
-        if constexpr (FMT == CPI_W_I4G32) {
-          const float b = chunk_bias<FMT>(xp);
+        if constexpr (kGroupScaled<FMT>) {
+          const float bias = chunk_bias<FMT>(xp);
 #pragma unroll
-          for (int i = 0; i < NR; ++i) acc[i] = fmaf(h2f(gsc[i][q]), chunk_dot<FMT>(wv[i][q], xp, b), acc[i]);
+          for (int i = 0; i < NR; ++i) acc[i] = fmaf(b.gsc[q].scale(i), chunk_dot<FMT>(b.wv[i][q], xp, bias), acc[i]);
         } else {
           if constexpr (FMT != CPI_W_F16) bias_sum += chunk_bias<FMT>(xp);
 #pragma unroll
-          for (int i = 0; i < NR; ++i) acc[i] = chunk_dot<FMT>(wv[i][q], xp, acc[i]);
+          for (int i = 0; i < NR; ++i) acc[i] = chunk_dot<FMT>(b.wv[i][q], xp, acc[i]);
         }
       }
     }
   };
-  compute(0);
-  for (int grp = 1; grp < g.ng; ++grp) {
-    issue(grp);
-    compute(grp);
+  if constexpr (DB) {
+    // the trip count is wave-uniform and every issue is unconditional inside
+    // its straight-line block, so each compute waits only for its own group
+    int k = 1;
+    for (; k + 1 < g.ng; k += 2) {
+      issue(k, gb);
+      compute(k - 1, ga);
+      issue(k + 1, ga);
+      compute(k, gb);
+    }
+    if (k < g.ng) {
+      issue(k, gb);
+      compute(k - 1, ga);
+      compute(k, gb);
+    } else {
+      compute(k - 1, ga);
+    }
+  } else {
+    compute(0, ga);
+    for (int grp = 1; grp < g.ng; ++grp) {
+      issue(grp, ga);
+      compute(grp, ga);
+    }
   }
   if constexpr (FMT == CPI_W_I8ROW || FMT == CPI_W_I4ROW) {
 #pragma unroll
@@ -711,17 +771,17 @@ size_t lds_bytes(int K) {
   return static_cast<size_t>(K / FmtT<FMT>::kElems) * FmtT<FMT>::kStride * sizeof(uint32_t);
 }
 
-template <int FMT, bool XF32, int NR, int PP, int MAXU, bool FOLD = false, bool GATHER = false>
+template <int FMT, bool XF32, int NR, int PP, int MAXU, bool FOLD = false, bool GATHER = false, bool DB = false>
 hipError_t launch_kernel(const GemvParams& p, int epi, const GemvPlan& g, size_t lds, hipStream_t s) {
   static size_t lds_set = 0;  // per instantiation: raise the dynamic-LDS limit once
   if (lds > 64 * 1024 && lds > lds_set) {
-    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<FMT, XF32, NR, PP, MAXU, FOLD, GATHER>),
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemv_kernel<FMT, XF32, NR, PP, MAXU, FOLD, GATHER, DB>),
                                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
     if (e != hipSuccess) return e;
     lds_set = lds;
   }
   const int slots = GATHER ? p.num_slots : 1;
-  hipLaunchKernelGGL((gemv_kernel<FMT, XF32, NR, PP, MAXU, FOLD, GATHER>), dim3(g.grid, slots), dim3(kBlock), lds, s, p, epi, g.ks);
+  hipLaunchKernelGGL((gemv_kernel<FMT, XF32, NR, PP, MAXU, FOLD, GATHER, DB>), dim3(g.grid, slots), dim3(kBlock), lds, s, p, epi, g.ks);
   return hipGetLastError();
 }
 
@@ -732,11 +792,15 @@ hipError_t launch_shape(const GemvParams& p, int epi, const GemvPlan& g, size_t 
   if constexpr (XF32) {
     if (p.add_k > 0) return launch_kernel<FMT, XF32, NR, PP, 2, true>(p, epi, g, lds, s);
   }
+  // K > 4096: several groups per wave, double-buffered
+  const bool db = g.ng > 1;
   if (p.expert_idx != nullptr) {
     if (p.K <= 2 * 8 * kBlock) return launch_kernel<FMT, XF32, NR, PP, 2, false, true>(p, epi, g, lds, s);
+    if (db) return launch_kernel<FMT, XF32, NR, PP, 8, false, true, true>(p, epi, g, lds, s);
     return launch_kernel<FMT, XF32, NR, PP, 8, false, true>(p, epi, g, lds, s);
   }
   if (p.K <= 2 * 8 * kBlock) return launch_kernel<FMT, XF32, NR, PP, 2>(p, epi, g, lds, s);
+  if (db) return launch_kernel<FMT, XF32, NR, PP, 8, false, false, true>(p, epi, g, lds, s);
   return launch_kernel<FMT, XF32, NR, PP, 8>(p, epi, g, lds, s);
 }
 
@@ -786,6 +850,7 @@ hipError_t gemv_launch(int wfmt, int epi, bool xf32, const GemvParams& p, hipStr
     case CPI_W_I8ROW: return dispatch_x<CPI_W_I8ROW>(epi, xf32, p, s);
     case CPI_W_I4ROW: return dispatch_x<CPI_W_I4ROW>(epi, xf32, p, s);
     case CPI_W_I4G32: return dispatch_x<CPI_W_I4G32>(epi, xf32, p, s);
+    case CPI_W_I4G32B: return dispatch_x<CPI_W_I4G32B>(epi, xf32, p, s);
   }
   return hipErrorInvalidValue;
 }
@@ -795,7 +860,8 @@ int gemv_elems_per_chunk(int wfmt) {
     case CPI_W_F16: return 8;
     case CPI_W_I8ROW: return 16;
     case CPI_W_I4ROW:
-    case CPI_W_I4G32: return 32;
+    case CPI_W_I4G32:
+    case CPI_W_I4G32B: return 32;
   }
   return 0;
 }

@@ -146,4 +146,23 @@ CPI_HD inline size_t scale_index(const GemvPlan& g, int row_c, int chunk_c) {
   return static_cast<size_t>(row_c) * static_cast<size_t>(g.nchunks) + static_cast<size_t>(chunk_c);
 }
 
+// Blocked group scales (CPI_W_I4G32B): the fp16 scale of (row r, chunk c) is
+// element ((r / 8) * nchunks + c) * 8 + r % 8, rows padded to a multiple of 8,
+// so the NR (<= 8, a power of two) rows of a wave share one NR * 2-byte load.
+constexpr int kScaleBlockRows = 8;
+// First row of the NR-row group holding row0, kept inside the padded rows.
+CPI_HD inline int clamp_row_group(const GemvPlan& g, int row0, int nr) {
+  const int last = ((g.R - 1) / nr) * nr;
+  return row0 < last ? row0 : last;
+}
+CPI_HD inline size_t scale_block_index(const GemvPlan& g, int row_c, int chunk_c) {
+  return (static_cast<size_t>(row_c / kScaleBlockRows) * static_cast<size_t>(g.nchunks) + static_cast<size_t>(chunk_c)) *
+             kScaleBlockRows +
+         static_cast<size_t>(row_c % kScaleBlockRows);
+}
+// Elements of a blocked scale tensor for R rows of `groups` groups.
+CPI_HD inline size_t blocked_scale_elems(int R, int groups) {
+  return static_cast<size_t>((R + kScaleBlockRows - 1) / kScaleBlockRows) * kScaleBlockRows * static_cast<size_t>(groups);
+}
+
 }  // namespace cpi

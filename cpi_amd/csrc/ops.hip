@@ -388,4 +388,18 @@ __global__ void gather_rows_kernel(const uint8_t* src, uint8_t* dst, const int* 
   }
 }
 
+// Row-major group scales [rows, groups] -> blocked by 8 rows (element
+// ((r / 8) * groups + g) * 8 + r % 8); padding rows are zero.  One thread per
+// destination element, so every element is written.
+__global__ void block_group_scales_kernel(const uint16_t* src, uint16_t* dst, int rows, int groups) {
+  const size_t n = static_cast<size_t>((rows + 7) / 8) * 8 * static_cast<size_t>(groups);
+  for (size_t e = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; e < n;
+       e += static_cast<size_t>(gridDim.x) * blockDim.x) {
+    const size_t blk = e / (8 * static_cast<size_t>(groups));
+    const int gi = static_cast<int>((e / 8) % static_cast<size_t>(groups));
+    const int r = static_cast<int>(blk * 8 + e % 8);
+    dst[e] = r < rows ? src[static_cast<size_t>(r) * groups + gi] : uint16_t{0};
+  }
+}
+
 }  // namespace cpi

@@ -152,6 +152,7 @@ template <> struct PW<CPI_W_F16> { static constexpr int kVec = 4; };    // 64 B
 template <> struct PW<CPI_W_I8ROW> { static constexpr int kVec = 2; };  // 32 B
 template <> struct PW<CPI_W_I4ROW> { static constexpr int kVec = 1; };  // 16 B
 template <> struct PW<CPI_W_I4G32> : PW<CPI_W_I4ROW> {};
+template <> struct PW<CPI_W_I4G32B> : PW<CPI_W_I4ROW> {};
 
 // Offset-binary bytes (b' = q + 128) or nibbles (n' = q + 8) sit under the
 // exponent of 1024.0 as fp16; subtracting the bias gives q exactly.
@@ -187,7 +188,7 @@ __device__ __forceinline__ h8 dequant8(const u32x4* raw, int s, f16x2 sc) {
     for (int b = 0; b < 4; ++b) {
       const uint32_t sel = 0x0c000c00u | (static_cast<uint32_t>(b + 4) << 16) | static_cast<uint32_t>(b);
       f16x2 q = as_h2(pair_bits(hi, lo, sel)) + bias;
-      if constexpr (FMT == CPI_W_I4G32) q = q * sc;
+      if constexpr (kGroupScaled<FMT>) q = q * sc;
       o[b] = __builtin_bit_cast(uint32_t, q);
     }
     out = u32x4{o[0], o[1], o[2], o[3]};
@@ -301,11 +302,17 @@ __global__ void __launch_bounds__(256) pgemm_kernel(PGemmParams p) {
   const uint32_t wvoff = (wr0 + c) * row_bytes + g * (WV * 16);
   const uint32_t gstride = static_cast<uint32_t>(K / 32) * 2u;   // scale bytes per row
   __amdgpu_buffer_rsrc_t grs = wrs;
-  if constexpr (FMT == CPI_W_I4G32)
+  if constexpr (kGroupScaled<FMT>)
     grs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(static_cast<const uint8_t*>(p.scales)) + static_cast<size_t>(n0) * gstride, 0,
-        rows_left * gstride, 0x00020000);
-  const uint32_t gvoff = (wr0 + c) * gstride + 2u * g;
+        (FMT == CPI_W_I4G32B ? (rows_left + 7) / 8 * 8 : rows_left) * gstride, 0x00020000);
+  // row-major [R, K/32]: row r at r * gstride; blocked by 8 rows: the 16 rows
+  // of an i step are two whole blocks (the same 16 * gstride bytes), and chunk
+  // ch of row r sits at ((r / 8) * (K/32) + ch) * 16 + (r % 8) * 2
+  constexpr bool kBlk = FMT == CPI_W_I4G32B;
+  const uint32_t gvoff = kBlk ? ((wr0 + c) >> 3) * 8u * gstride + ((wr0 + c) & 7) * 2u + 16u * g
+                              : (wr0 + c) * gstride + 2u * g;
+  constexpr int kGStep = kBlk ? 4 * 16 : 8;  // scale bytes per 128-k step
   struct WRegs {
     u32x4 w[RB][WV];
     f16x2 sc[RB];
@@ -318,9 +325,9 @@ __global__ void __launch_bounds__(256) pgemm_kernel(PGemmParams p) {
 #pragma unroll
       for (int v = 0; v < WV; ++v)
         r.w[i][v] = __builtin_amdgcn_raw_buffer_load_b128(wrs, wvoff, 16 * i * row_bytes + kt * kStepBytes + 16 * v, 0);
-      if constexpr (FMT == CPI_W_I4G32) {
+      if constexpr (kGroupScaled<FMT>) {
         const f16 s = __builtin_bit_cast(
-            f16, __builtin_amdgcn_raw_buffer_load_b16(grs, gvoff, 16 * i * gstride + kt * 8, 0));
+            f16, __builtin_amdgcn_raw_buffer_load_b16(grs, gvoff, 16 * i * gstride + kt * kGStep, 0));
         r.sc[i] = f16x2{s, s};
       }
     }
@@ -779,6 +786,7 @@ hipError_t pgemm_launch(int wfmt, PGemmParams p, void* workspace, size_t workspa
     case CPI_W_I8ROW: return pgemm_launch_fmt<CPI_W_I8ROW>(p, pl, grid, s);
     case CPI_W_I4ROW: return pgemm_launch_fmt<CPI_W_I4ROW>(p, pl, grid, s);
     case CPI_W_I4G32: return pgemm_launch_fmt<CPI_W_I4G32>(p, pl, grid, s);
+    case CPI_W_I4G32B: return pgemm_launch_fmt<CPI_W_I4G32B>(p, pl, grid, s);
     default: return hipErrorInvalidValue;
   }
 }

@@ -144,7 +144,9 @@ std::size_t LlamaEngine::weight_bytes_of(const Linear& L) {
 }
 
 std::size_t LlamaEngine::scale_bytes_of(const Linear& L) {
-  if (L.wfmt == CPI_W_I4G32) return static_cast<std::size_t>(L.rows) * ((L.cols + 31) / 32) * 2;
+  // group scales are resident in the blocked layout (CPI_W_I4G32B)
+  if (L.wfmt == CPI_W_I4G32 || L.wfmt == CPI_W_I4G32B)
+    return cpi_hip_blocked_scale_count(L.rows, (L.cols + 31) / 32) * 2;
   if (L.wfmt == CPI_W_F16) return 0;
   return static_cast<std::size_t>(L.rows) * 4;
 }
@@ -193,10 +195,24 @@ LlamaEngine::Linear LlamaEngine::upload_fused(const std::vector<HostLinear>& par
   (void)total;
 
   if (L.wfmt == CPI_W_I4G32) {
+    // row-major [R, K/32] as in the file, then blocked by 8 rows on the
+    // device: a GEMV wave then reads its 8 rows' scales with one 16-byte load
     std::vector<std::pair<const std::byte*, std::size_t>> sblocks;
     for (const auto& p : parts) sblocks.push_back({p.scales, p.scale_bytes});
-    L.scales = place(sblocks, ((K + 31) / 32) * 2, dst_s);
-    L.scale_count = L.rows * static_cast<int>((K + 31) / 32);
+    const int groups = static_cast<int>((K + 31) / 32);
+    void* rowmajor = nullptr;
+    HIP_OK(hipMalloc(&rowmajor, static_cast<std::size_t>(L.rows) * groups * 2));
+    place(sblocks, static_cast<std::size_t>(groups) * 2, rowmajor);
+    weight_bytes_ -= static_cast<std::size_t>(L.rows) * groups * 2;  // counted below in blocked form
+    const std::size_t blocked = cpi_hip_blocked_scale_count(L.rows, groups) * 2;
+    L.scales = dst_s ? dst_s : dmalloc(blocked);
+    weight_bytes_ += blocked;
+    CPI_OK(cpi_hip_block_group_scales(static_cast<const uint16_t*>(rowmajor), static_cast<uint16_t*>(L.scales),
+                                      L.rows, groups, stream_));
+    HIP_OK(hipStreamSynchronize(stream_));
+    HIP_OK(hipFree(rowmajor));
+    L.wfmt = CPI_W_I4G32B;
+    L.scale_count = L.rows * groups;
   } else if (L.wfmt != CPI_W_F16) {
     // per-row fp32 scales (a single global scale is expanded per row)
     std::vector<float> s;
@@ -441,8 +457,8 @@ void LlamaEngine::setup_fused() {
   if (!env || std::string(env) != "1") return;
   if (cfg_.is_moe() || lm_head_.wfmt != CPI_W_F16) return;
   for (const auto& L : layers_)
-    if (L.qkv.wfmt != CPI_W_I4G32 || L.wo.wfmt != CPI_W_I4G32 || L.w13.wfmt != CPI_W_I4G32 ||
-        L.w2.wfmt != CPI_W_I4G32)
+    if (L.qkv.wfmt != CPI_W_I4G32B || L.wo.wfmt != CPI_W_I4G32B || L.w13.wfmt != CPI_W_I4G32B ||
+        L.w2.wfmt != CPI_W_I4G32B)
       return;
   std::vector<cpi_fused_layer> table(layers_.size());
   for (std::size_t l = 0; l < layers_.size(); ++l) {

@@ -17,12 +17,13 @@ from cpi_amd import _lib
 # (name, R, K): Llama-2-7B projection shapes
 GEMV_SHAPES = [("qkv", 12288, 4096), ("w13", 22016, 4096), ("w2", 4096, 11008), ("o_proj", 4096, 4096)]
 
-FMT_CODE = {"f16": _lib.W_F16, "i8": _lib.W_I8ROW, "i4": _lib.W_I4ROW, "i4g32": _lib.W_I4G32}
+FMT_CODE = {"f16": _lib.W_F16, "i8": _lib.W_I8ROW, "i4": _lib.W_I4ROW, "i4g32": _lib.W_I4G32,
+            "i4g32b": _lib.W_I4G32B}
 
 
 def gemv_bytes(fmt: str, R: int, K: int) -> int:
     """Algorithmic HBM bytes of one launch: weights + scales + x (fp16) + y (fp16)."""
-    if fmt == "i4g32":
+    if fmt in ("i4g32", "i4g32b"):
         w = R * K // 2 + R * (K // 32) * 2
     elif fmt == "i4":
         w = R * K // 2 + 4 * R
@@ -34,15 +35,20 @@ def gemv_bytes(fmt: str, R: int, K: int) -> int:
 
 
 def _weights(fmt, R, K, gen):
-    if fmt in ("i4", "i4g32"):
+    if fmt in ("i4", "i4g32", "i4g32b"):
         w = torch.randint(0, 256, (R * K // 2,), dtype=torch.uint8, device="cuda", generator=gen)
     elif fmt == "i8":
         w = torch.randint(0, 256, (R * K,), dtype=torch.uint8, device="cuda", generator=gen)
     else:
         w = (torch.randn(R * K, device="cuda", generator=gen) * 0.02).half().view(torch.uint8)
-    if fmt == "i4g32":
+    if fmt in ("i4g32", "i4g32b"):
         s = (torch.randn(R * K // 32, device="cuda", generator=gen).abs() * 0.01).half()
         sc = s.numel()
+        if fmt == "i4g32b":  # the engine's resident layout: blocked by 8 rows
+            b = torch.empty(_lib.lib().cpi_hip_blocked_scale_count(R, K // 32), dtype=torch.float16, device="cuda")
+            st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+            _lib.call("cpi_hip_block_group_scales", s.data_ptr(), b.data_ptr(), R, K // 32, st)
+            s = b
     elif fmt in ("i4", "i8"):
         s = torch.rand(R, device="cuda", generator=gen) * 0.01
         sc = R
@@ -51,20 +57,30 @@ def _weights(fmt, R, K, gen):
     return w, s, sc
 
 
-def time_gemv(fmt: str, R: int, K: int, rotate_bytes: int = 3 << 30, iters: int = 200):
-    """Returns dict(us=avg per launch, gbps=algorithmic GB/s)."""
+def time_gemv(fmt: str, R: int, K: int, rotate_bytes: int = 3 << 30, iters: int = 200, swiglu: bool = False):
+    """Returns dict(us=avg per launch, gbps=algorithmic GB/s).  swiglu=True
+    times the decode engine's w1|w3 launch: fp32 residual input, RMSNorm
+    prologue (fp16 norm weights), SiLU(w1 x) * (w3 x) epilogue to R/2 fp16."""
     gen = torch.Generator(device="cuda").manual_seed(R + K)
     nbytes = gemv_bytes(fmt, R, K)
+    if swiglu:  # fp32 x and norm weights in, R/2 fp16 out
+        nbytes += 2 * K + 2 * K - R
     copies = max(2, int(np.ceil(rotate_bytes / nbytes)))
     bufs = [_weights(fmt, R, K, gen) for _ in range(copies)]
-    x = torch.randn(K, device="cuda", generator=gen).half()
+    if swiglu:
+        x = torch.randn(K, device="cuda", generator=gen)
+        nw = (1 + 0.1 * torch.randn(K, device="cuda", generator=gen)).half()
+    else:
+        x = torch.randn(K, device="cuda", generator=gen).half()
     y = torch.empty(R, device="cuda", dtype=torch.float16)
     descs = []
     for w, s, sc in bufs:
         d = _lib.GemvDesc()
         d.wfmt, d.w, d.scales, d.scale_count = FMT_CODE[fmt], w.data_ptr(), (s.data_ptr() if s is not None else 0), sc
-        d.out_features, d.in_features, d.x, d.x_is_f32 = R, K, x.data_ptr(), 0
-        d.epilogue, d.y = _lib.EPI_STORE_F16, y.data_ptr()
+        d.out_features, d.in_features, d.x, d.x_is_f32 = R, K, x.data_ptr(), int(swiglu)
+        d.epilogue, d.y = (_lib.EPI_SWIGLU_F16 if swiglu else _lib.EPI_STORE_F16), y.data_ptr()
+        if swiglu:
+            d.norm_w, d.norm_eps = nw.data_ptr(), 1e-5
         descs.append(d)
     fn = _lib.lib().cpi_hip_gemv
 
@@ -191,7 +207,8 @@ def pmc_workload(copy_mib: int = 512, launches: int = 20):
     """Eager launches for `rocprofv3 --pmc` runs (counters are read per
     dispatch): `launches` plain device-to-device copies of `copy_mib` MiB (the
     calibration kernel: it moves exactly 2 x copy_mib MiB), then `launches`
-    w1|w3 int4-g32 GEMVs (22016 x 4096) over distinct weight copies."""
+    w1|w3 int4-g32 GEMVs (22016 x 4096, blocked scales as resident in the engine)
+    over distinct weight copies."""
     src = torch.empty(copy_mib << 20, dtype=torch.uint8, device="cuda").random_(0, 256)
     dst = torch.empty_like(src)
     for _ in range(launches):
@@ -205,9 +222,9 @@ def pmc_workload(copy_mib: int = 512, launches: int = 20):
     fn = _lib.lib().cpi_hip_gemv
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     for i in range(launches):
-        w, s, sc = _weights("i4g32", R, K, gen)
+        w, s, sc = _weights("i4g32b", R, K, gen)
         d = _lib.GemvDesc()
-        d.wfmt, d.w, d.scales, d.scale_count = _lib.W_I4G32, w.data_ptr(), s.data_ptr(), sc
+        d.wfmt, d.w, d.scales, d.scale_count = _lib.W_I4G32B, w.data_ptr(), s.data_ptr(), sc
         d.out_features, d.in_features, d.x, d.x_is_f32 = R, K, x.data_ptr(), 0
         d.epilogue, d.y = _lib.EPI_STORE_F16, y.data_ptr()
         torch.cuda.synchronize()

@@ -44,13 +44,26 @@ int cpi_hip_can_fit_on_device(size_t bytes, size_t safety_margin_bytes); /* 1 / 
  *                   two's complement, + fp32 scale per row       (.int4/.scale)
  *     CPI_W_I4G32   same packing + fp16 scale per 32-column group
  *                   [R, K/32]                                    (.int4/.gscale)
+ *     CPI_W_I4G32B  same packing + the same fp16 group scales blocked by
+ *                   8 rows: scale (r, g) at ((r/8)*(K/32) + g)*8 + r%8,
+ *                   rows padded to a multiple of 8 (the resident layout of
+ *                   the engine; see cpi_hip_block_group_scales)
  *   A scale tensor holding ONE fp32 value (global scale) is accepted for the
  *   row formats by passing scale_count = 1.
  *   x is fp16 or fp32 (x_is_f32); accumulation is fp32.
  *   Preconditions: in_features % 32 == 0 (I4*), % 16 (I8ROW), % 8 (F16);
  *   weights 16-byte aligned.
  * ---------------------------------------------------------------------- */
-enum { CPI_W_F16 = 0, CPI_W_I8ROW = 1, CPI_W_I4ROW = 2, CPI_W_I4G32 = 3 };
+enum { CPI_W_F16 = 0, CPI_W_I8ROW = 1, CPI_W_I4ROW = 2, CPI_W_I4G32 = 3, CPI_W_I4G32B = 4 };
+
+/* Row-major fp16 group scales [rows, groups] (CPI_W_I4G32) -> the blocked
+ * layout of CPI_W_I4G32B; dst holds cpi_hip_blocked_scale_count(rows, groups)
+ * fp16 values (padding rows are written as zero).  No reference counterpart:
+ * the reference streams [R, K/32] scales per lane; the blocked layout lets a
+ * wave fetch the scales of its 8 rows with one 16-byte load per lane. */
+size_t cpi_hip_blocked_scale_count(int rows, int groups);
+int cpi_hip_block_group_scales(const uint16_t* src, uint16_t* dst, int rows,
+                               int groups, cpi_stream_t stream);
 
 /* y[r] = fp16(scale[r] * sum_k q[r,k] x[k])
  * replaces launch_weight_only_int4_matvec (kernels.cuh:649-656) and, with

@@ -1,6 +1,7 @@
 // Host replay of the GEMV kernel's load/compute schedule (cpi_amd/csrc/gemv_plan.hpp):
-// every weight / scale address must be in bounds and every (row, chunk) pair of
-// the matrix must be accumulated exactly once.
+// every weight / scale address (row-major and blocked group scales) must be in
+// bounds and every (row, chunk) pair of the matrix must be accumulated exactly
+// once, with its own scale.
 // Usage: gemv_addr_check R K elems force_shape force_ks
 #include <cstdio>
 #include <cstdlib>
@@ -21,6 +22,7 @@ int main(int argc, char** argv) {
   }
   const size_t wbytes = static_cast<size_t>(R) * g.row_bytes;
   const size_t nscales = static_cast<size_t>(R) * g.nchunks;
+  const size_t nblocked = blocked_scale_elems(R, g.nchunks);
   std::vector<int> hits(static_cast<size_t>(R) * g.nchunks, 0);
   long loads = 0;
   for (int block = 0; block < g.grid; ++block)
@@ -32,6 +34,14 @@ int main(int argc, char** argv) {
           const int pass = clamp_pass(g, sg, pass_u);
           for (int lane = 0; lane < 64; ++lane) {
             const int c = clamp_chunk(g, pass, lane);
+            // blocked scales: one load of nr elements from the row group's first row
+            const int row0 = plan_row(g, block, rs, 0);
+            const size_t sb = scale_block_index(g, clamp_row_group(g, row0, g.nr), c);
+            if (sb + g.nr > nblocked || sb % g.nr != 0) {
+              printf("blocked scale load OOB/misaligned R=%d K=%d block=%d wave=%d lane=%d at %zu/%zu\n", R, K, block,
+                     wave, lane, sb, nblocked);
+              return 1;
+            }
             for (int i = 0; i < g.nr; ++i) {
               const int row_u = plan_row(g, block, rs, i);
               const int row = clamp_row(g, row_u);
@@ -48,6 +58,10 @@ int main(int argc, char** argv) {
               if (pass_valid(g, sg, pass_u) && cu < g.nchunks && row_u < R) {
                 if (cu != c || row_u != row) {
                   printf("clamped load accumulated\n");
+                  return 1;
+                }
+                if (sb + i != scale_block_index(g, row, c)) {
+                  printf("blocked scale of row %d chunk %d read from the wrong element\n", row, c);
                   return 1;
                 }
                 ++hits[static_cast<size_t>(row) * g.nchunks + c];

@@ -53,3 +53,20 @@ def gemv(fmt: int, w, scales, scale_count, R, K, x, y, epilogue=_lib.EPI_STORE_F
     for k, v in kw.items():
         setattr(d, k, v.data_ptr() if isinstance(v, torch.Tensor) else v)
     _lib.call("cpi_hip_gemv", ctypes.byref(d), stream())
+
+
+def block_scales(s: np.ndarray, R: int, groups: int) -> np.ndarray:
+    """Row-major fp16 group scales [R, groups] in the blocked layout of
+    CPI_W_I4G32B: element ((r // 8) * groups + g) * 8 + r % 8, rows padded to a
+    multiple of 8 with zeros."""
+    rp = (R + 7) // 8 * 8
+    a = np.zeros((rp, groups), np.float16)
+    a[:R] = np.asarray(s, np.float16).reshape(R, groups)
+    return np.ascontiguousarray(a.reshape(rp // 8, 8, groups).transpose(0, 2, 1)).reshape(-1)
+
+
+def device_scales(fmt: str, s, R: int, K: int):
+    """Scales as the device expects them for `fmt` (numpy, or None)."""
+    if s is None:
+        return None
+    return block_scales(s, R, K // 32) if fmt == "i4g32b" else s

@@ -52,7 +52,7 @@ def build(nl, H, I, V, nh, nkv, hd, max_ctx, pos, window, seed):
         L = {"host": {}}
         for nm, R, K in (("qkv", qkv_rows, H), ("o", H, nh * hd), ("w13", 2 * I, H), ("w2", H, I)):
             w, s = i4g32(rng, R, K, sstd)
-            L[nm] = (G.dev(w), G.dev(s))
+            L[nm] = (G.dev(w), G.dev(G.block_scales(s, R, K // 32)))  # the engine's blocked layout
             L["host"][nm] = (w, s)
         L["na"] = G.dev((1 + 0.1 * rng.standard_normal(H)).astype(np.float16))
         L["nf"] = G.dev((1 + 0.1 * rng.standard_normal(H)).astype(np.float16))
@@ -125,18 +125,18 @@ def run_ops(m, st):
     qkv_rows = (nh + 2 * nkv) * hd
     _lib.call("cpi_hip_embedding_lookup_f32", G.ptr(m["emb"]), G.ptr(st["token"]), G.ptr(st["x"]), 1, H, G.stream())
     for i, L in enumerate(m["layers"]):
-        G.gemv(_lib.W_I4G32, L["qkv"][0], L["qkv"][1], qkv_rows * H // 32, qkv_rows, H, st["x"], st["q"],
+        G.gemv(_lib.W_I4G32B, L["qkv"][0], L["qkv"][1], qkv_rows * H // 32, qkv_rows, H, st["x"], st["q"],
                epilogue=_lib.EPI_QKV_ROPE, norm_w=L["na"], num_heads=nh, num_kv_heads=nkv, head_dim=hd,
                position=st["pos"], rope_cos=m["cos"], rope_sin=m["sin"], k_cache=st["kc"][i], v_cache=st["vc"][i],
                max_context=m["max_ctx"])
         _lib.call("cpi_hip_attention_decode", G.ptr(st["q"]), 1, G.ptr(st["kc"][i]), G.ptr(st["vc"][i]),
                   G.ptr(st["att"]), 1, 0, G.ptr(st["pos"]), nh, nkv, hd, m["max_ctx"], m["window"],
                   G.ptr(st["scratch"]), G.stream())
-        G.gemv(_lib.W_I4G32, L["o"][0], L["o"][1], H * nh * hd // 32, H, nh * hd, st["att"], st["x"],
+        G.gemv(_lib.W_I4G32B, L["o"][0], L["o"][1], H * nh * hd // 32, H, nh * hd, st["att"], st["x"],
                epilogue=_lib.EPI_RESID_ADD)
-        G.gemv(_lib.W_I4G32, L["w13"][0], L["w13"][1], 2 * I * H // 32, 2 * I, H, st["x"], st["ff"],
+        G.gemv(_lib.W_I4G32B, L["w13"][0], L["w13"][1], 2 * I * H // 32, 2 * I, H, st["x"], st["ff"],
                epilogue=_lib.EPI_SWIGLU, norm_w=L["nf"])
-        G.gemv(_lib.W_I4G32, L["w2"][0], L["w2"][1], H * I // 32, H, I, st["ff"], st["x"],
+        G.gemv(_lib.W_I4G32B, L["w2"][0], L["w2"][1], H * I // 32, H, I, st["ff"], st["x"],
                epilogue=_lib.EPI_RESID_ADD)
     G.gemv(_lib.W_F16, m["lm"], None, 0, V, H, st["x"], st["logits"], epilogue=_lib.EPI_STORE_F32, norm_w=m["nout"])
     _lib.call("cpi_hip_greedy_advance", G.ptr(st["logits"]), V, G.ptr(st["token"]), G.ptr(st["pos"]),

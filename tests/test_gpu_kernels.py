@@ -14,11 +14,13 @@ pytestmark = pytest.mark.gpu
 if torch.cuda.is_available():
     from tests import gpu_util as G
 
-FMTS = {"f16": _lib.W_F16, "i8": _lib.W_I8ROW, "i4": _lib.W_I4ROW, "i4g32": _lib.W_I4G32}
+FMTS = {"f16": _lib.W_F16, "i8": _lib.W_I8ROW, "i4": _lib.W_I4ROW, "i4g32": _lib.W_I4G32, "i4g32b": _lib.W_I4G32B}
 
 
 def make_weights(fmt, R, K, seed, random_lowbit=False):
     """Returns (blob uint8, scales array or None, dequantised fp32 [R,K])."""
+    if fmt == "i4g32b":  # the same weights; only the device layout of the scales differs
+        fmt = "i4g32"
     rng = np.random.default_rng(seed)
     if fmt == "i4g32" and random_lowbit:
         blob = rng.integers(0, 256, R * K // 2, dtype=np.uint8)
@@ -62,13 +64,57 @@ def test_gemv_parity(fmt, R, K):
     assert (np.abs(got - ref) <= bound).all(), np.abs(got - ref).max()
 
 
-@pytest.mark.parametrize("fmt", ["i8", "i4", "i4g32"])
+@pytest.mark.parametrize("R,groups", [(8, 1), (300, 17), (22016, 128), (13, 4)])
+def test_block_group_scales(R, groups):
+    """Device repack into the blocked layout equals its numpy restatement
+    (padding rows zero) and the element count matches the library's."""
+    s = np.random.default_rng(R).standard_normal(R * groups).astype(np.float16)
+    n = _lib.lib().cpi_hip_blocked_scale_count(R, groups)
+    assert n == (R + 7) // 8 * 8 * groups
+    dst = G.dev(np.full(n, np.float16(7.0)))
+    _lib.call("cpi_hip_block_group_scales", G.ptr(G.dev(s)), G.ptr(dst), R, groups, G.stream())
+    got = G.host(dst, np.uint16, n)
+    want = G.block_scales(s, R, groups).view(np.uint16)
+    np.testing.assert_array_equal(got, want)
+    r, g = R - 1, groups - 1  # spot check of the formula itself
+    assert got[((r // 8) * groups + g) * 8 + r % 8] == s.view(np.uint16)[r * groups + g]
+
+
+@pytest.mark.parametrize("form", ["plain_f32", "plain_f16", "norm_swiglu", "norm_f16out"])
+@pytest.mark.parametrize("R,K", [(40, 96), (8, 32), (300, 544), (1000, 4096), (22016, 4096), (4096, 11008),
+                                 (4096, 4096)])
+def test_gemv_blocked_scales_match_rowmajor(R, K, form):
+    """CPI_W_I4G32B (blocked scales) gives the same bits as CPI_W_I4G32 on the
+    same weights: only the scale addressing differs."""
+    print(f"[gemv-blocked] R={R} K={K} form={form}", flush=True)
+    if form == "norm_swiglu" and R % 8:
+        pytest.skip("SWIGLU needs whole 8-row tiles")
+    blob, sc, _ = make_weights("i4g32", R, K, R * 3 + K, random_lowbit=True)
+    rng = np.random.default_rng(K + 1)
+    x = rng.standard_normal(K).astype(np.float32)
+    xd = G.dev(x if form != "plain_f16" else x.astype(np.float16))
+    kw = {}
+    epi = _lib.EPI_STORE_F32
+    if form.startswith("norm"):
+        kw["norm_w"] = G.dev((1 + 0.1 * rng.standard_normal(K)).astype(np.float16))
+        epi = _lib.EPI_SWIGLU if form == "norm_swiglu" else _lib.EPI_STORE_F16
+    w = G.dev(blob)
+    outs = []
+    for fmt in ("i4g32", "i4g32b"):
+        y = G.empty(R * 4)
+        G.gemv(FMTS[fmt], w, G.dev(G.device_scales(fmt, sc, R, K)), sc.size, R, K, xd, y, epilogue=epi,
+               x_f32=(form != "plain_f16"), **kw)
+        outs.append(G.host(y, np.uint32, R).copy())
+    np.testing.assert_array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("fmt", ["i8", "i4", "i4g32", "i4g32b"])
 def test_gemv_unpack_bit_exact(fmt):
     """A one-hot x makes the GEMV return column k of the dequantised matrix:
     q * scale computed exactly, so the result must match bit for bit."""
     R, K = 64, 128
     blob, sc, deq = make_weights(fmt, R, K, 11)
-    w, s = G.dev(blob), G.dev(sc)
+    w, s = G.dev(blob), G.dev(G.device_scales(fmt, sc, R, K))
     for k in (0, 1, 7, 8, 31, 32, 63, 127):
         x = np.zeros(K, np.float32)
         x[k] = 1.0
@@ -150,11 +196,11 @@ def test_gemv_swiglu(fmt):
 
 
 def _split_rows(blob, sc, fmt, R, K):
-    bpr = {"f16": 2 * K, "i8": K, "i4": K // 2, "i4g32": K // 2}[fmt]
+    bpr = {"f16": 2 * K, "i8": K, "i4": K // 2, "i4g32": K // 2, "i4g32b": K // 2}[fmt]
     w = blob.reshape(R, bpr)
     if sc is None:
         return w, None
-    return w, (sc.reshape(R, -1) if fmt == "i4g32" else sc.reshape(R, 1))
+    return w, (sc.reshape(R, -1) if fmt in ("i4g32", "i4g32b") else sc.reshape(R, 1))
 
 
 @pytest.mark.parametrize("fmt", ["f16", "i4g32", "i8"])
@@ -324,7 +370,7 @@ def test_moe_router_matches_oracle():
     np.testing.assert_allclose(G.host(prob, np.float32, K), rp, rtol=1e-5)
 
 
-@pytest.mark.parametrize("fmt", ["i4g32", "i8", "f16"])
+@pytest.mark.parametrize("fmt", ["i4g32", "i4g32b", "i8", "f16"])
 def test_moe_expert_gemv_and_combine(fmt):
     """Gathered expert GEMVs (both selected experts in one launch) equal the
     plain GEMV of each selected expert; combine adds sum_k p_k y_k."""
@@ -337,10 +383,10 @@ def test_moe_expert_gemv_and_combine(fmt):
         b, s, _ = make_weights(fmt, 2 * EI, H, 100 + e)
         wr, sr = _split_rows(b, s, fmt, 2 * EI, H)
         w13.append(np.ascontiguousarray(wr[order]))
-        s13.append(None if sr is None else np.ascontiguousarray(sr[order]))
+        s13.append(None if sr is None else G.device_scales(fmt, np.ascontiguousarray(sr[order]), 2 * EI, H))
         b2, s2_, _ = make_weights(fmt, H, EI, 200 + e)
         w2.append(b2)
-        s2.append(s2_)
+        s2.append(G.device_scales(fmt, s2_, H, EI))
     cat = lambda parts: np.concatenate([p.reshape(-1) for p in parts])
     W13, W2 = G.dev(cat(w13)), G.dev(cat(w2))
     S13 = None if s13[0] is None else G.dev(cat(s13))

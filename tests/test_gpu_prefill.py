@@ -47,7 +47,7 @@ def row_bound(fmt, deq, x):
 
 
 @pytest.mark.parametrize("split", [True, False])
-@pytest.mark.parametrize("fmt", ["f16", "i8", "i4", "i4g32"])
+@pytest.mark.parametrize("fmt", ["f16", "i8", "i4", "i4g32", "i4g32b"])
 @pytest.mark.parametrize("N,K,M", [(64, 64, 1), (200, 192, 7), (384, 512, 64), (1000, 1024, 130),
                                    (4096, 11008, 128)])
 def test_prefill_gemm_parity(fmt, N, K, M, split):
@@ -56,7 +56,8 @@ def test_prefill_gemm_parity(fmt, N, K, M, split):
     x16 = np.random.default_rng(M).standard_normal((M, K)).astype(np.float16)
     xf = x16.astype(np.float32)
     y = G.empty(M * N * 4)
-    wd, sd, xd = G.dev(blob), None if sc is None else G.dev(sc), G.dev(x16)
+    wd, sd, xd = G.dev(blob), None if sc is None else G.dev(G.device_scales(fmt, sc, N, K)), G.dev(x16)
+
     ws = gemm(fmt, wd, sd, 0 if sc is None else sc.size, N, K, xd, M, y, split=split)
     got = G.host(y, np.float32, M * N).reshape(M, N)
     if ws is not None:
@@ -67,14 +68,19 @@ def test_prefill_gemm_parity(fmt, N, K, M, split):
         y2 = G.empty(M * N * 4)
         gemm(fmt, wd, sd, 0 if sc is None else sc.size, N, K, xd, M, y2, split=split)
         assert np.array_equal(G.host(y2, np.float32, M * N).reshape(M, N), got)
+    if fmt == "i4g32b":  # blocked scales: the same bits as the row-major layout
+        y3 = G.empty(M * N * 4)
+        gemm("i4g32", wd, G.dev(sc), sc.size, N, K, xd, M, y3, split=split)
+        assert np.array_equal(G.host(y3, np.float32, M * N).reshape(M, N), got)
     rows = [0, M // 2, M - 1]
-    ref = np.stack([oracle.gemv(fmt, blob, sc, N, K, xf[m]) for m in rows])
-    bound = row_bound(fmt, deq, xf[rows])
+    ofmt = "i4g32" if fmt == "i4g32b" else fmt  # the oracle reads row-major scales
+    ref = np.stack([oracle.gemv(ofmt, blob, sc, N, K, xf[m]) for m in rows])
+    bound = row_bound(ofmt, deq, xf[rows])
     err = np.abs(got[rows] - ref)
     assert np.all(err <= bound), float((err / bound).max())
     # every token against a float64 product of the dequantised weights
     ref_all = xf.astype(np.float64) @ deq.astype(np.float64).T
-    assert np.all(np.abs(got - ref_all) <= row_bound(fmt, deq, xf) + 2e-5 * np.abs(ref_all))
+    assert np.all(np.abs(got - ref_all) <= row_bound(ofmt, deq, xf) + 2e-5 * np.abs(ref_all))
 
 
 def test_prefill_gemm_global_scale_and_resid():
