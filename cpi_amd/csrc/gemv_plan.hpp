@@ -29,6 +29,9 @@ constexpr int kPassChunks = 64;   // chunks per pass (one per lane)
 constexpr int kWavesPerBlock = 4;
 constexpr int kTileRows = 8;      // row granularity of the fused epilogues
 constexpr int kMaxLoads = 16;     // NR * PP: 16-byte loads a lane keeps in flight
+// Workgroups resident at once: 256 CUs x 4 (occupancy 4 waves per SIMD at the
+// ~100-112 VGPRs of the K <= 4096 instantiations).
+constexpr int kResidentWgs = 1024;
 
 // (NR, PP) shapes the kernel is instantiated for.
 struct WaveShape {
@@ -100,6 +103,13 @@ inline GemvPlan plan_launch(int R, int K, int elems, int force_shape, int force_
       const double util = static_cast<double>(g.np) / (static_cast<double>(g.ks) * g.ng * g.pp);
       const double waves = static_cast<double>(g.grid) * kWavesPerBlock * slots;
       double score = util * (waves >= 1024.0 ? 1.0 : waves / 1024.0);
+      // a mostly empty last round of workgroups starts only after the first
+      // round drains (one more HBM latency plus prologue, ~4 us measured for
+      // w1|w3 at 1376 workgroups = 1.34 rounds): score the fill of the rounds
+      const int wgs = g.grid * slots;
+      const int rounds = (wgs + kResidentWgs - 1) / kResidentWgs;
+      const double fill = static_cast<double>(wgs) / (static_cast<double>(rounds) * kResidentWgs);
+      if (rounds > 1 && fill < 0.9) score *= fill;
       score *= g.nr >= 8 ? 1.0 : (g.nr >= 4 ? 0.95 : 0.85);
       if (g.nr * g.pp < 8) score *= 0.9;
       // ties: more waves, then more rows per wave
