@@ -765,9 +765,10 @@ inline size_t pgemm_workspace_bytes(int N, int K, int M) {
 template <int FMT>
 hipError_t pgemm_launch_fmt(const PGemmParams& p, const PGemmPlan& pl, dim3 grid, hipStream_t s) {
   if (pl.mt == 128 && pl.rb == 2) hipLaunchKernelGGL((pgemm_kernel<FMT, 128, 2>), grid, dim3(256), 0, s, p);
-  else if (pl.mt == 128) hipLaunchKernelGGL((pgemm_kernel<FMT, 128, 1>), grid, dim3(256), 0, s, p);
-  else if (pl.rb == 2) hipLaunchKernelGGL((pgemm_kernel<FMT, 64, 2>), grid, dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((pgemm_kernel<FMT, 64, 1>), grid, dim3(256), 0, s, p);
+  else if (pl.mt == 128 && pl.rb == 1) hipLaunchKernelGGL((pgemm_kernel<FMT, 128, 1>), grid, dim3(256), 0, s, p);
+  else if (pl.mt == 64 && pl.rb == 2) hipLaunchKernelGGL((pgemm_kernel<FMT, 64, 2>), grid, dim3(256), 0, s, p);
+  else if (pl.mt == 64 && pl.rb == 1) hipLaunchKernelGGL((pgemm_kernel<FMT, 64, 1>), grid, dim3(256), 0, s, p);
+  else return hipErrorInvalidValue;  // no kernel for this tile: the plan and the table disagree
   return hipGetLastError();
 }
 
