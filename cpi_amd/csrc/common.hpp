@@ -16,6 +16,7 @@ constexpr bool kGroupScaled = FMT == CPI_W_I4G32 || FMT == CPI_W_I4G32B;
 typedef _Float16 f16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;
 

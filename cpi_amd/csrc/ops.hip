@@ -263,7 +263,32 @@ __device__ void block_argmax(const float* x, int n, float& bv, int& bi) {
   __shared__ int si[16];
   float v = -INFINITY;
   int idx = 0x7fffffff;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) argmax_merge(v, idx, x[i], i);
+  // 16-byte loads, all of a round issued before any is merged (a 32000-entry
+  // vocabulary is one round of 8 per thread); the merge is a total order
+  // (value, then lowest index; NaN never wins), so the visiting order does
+  // not change the result
+  constexpr int kU = 8;
+  const int n4 = (reinterpret_cast<uintptr_t>(x) & 15) == 0 ? n / 4 : 0;
+  const int nt = static_cast<int>(blockDim.x);
+  for (int base = 0; base < n4; base += kU * nt) {
+    f32x4 r[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int q = min(base + u * nt + static_cast<int>(threadIdx.x), n4 - 1);
+      r[u] = reinterpret_cast<const f32x4*>(x)[q];
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int q = base + u * nt + static_cast<int>(threadIdx.x);
+      if (q < n4) {
+        argmax_merge(v, idx, r[u].x, 4 * q);
+        argmax_merge(v, idx, r[u].y, 4 * q + 1);
+        argmax_merge(v, idx, r[u].z, 4 * q + 2);
+        argmax_merge(v, idx, r[u].w, 4 * q + 3);
+      }
+    }
+  }
+  for (int i = 4 * n4 + static_cast<int>(threadIdx.x); i < n; i += nt) argmax_merge(v, idx, x[i], i);
 #pragma unroll
   for (int m = 1; m < kWave; m <<= 1) {
     const float ov = __shfl_xor(v, m, kWave);

@@ -286,6 +286,50 @@ def test_attention_sliding_window():
     np.testing.assert_allclose(G.host(out, np.float32, nh * hd), ref, atol=2e-4)
 
 
+def _argmax_ref(x):
+    """std::max_element rule of the reference (cpu_engine.cpp:726-729) over
+    the non-NaN entries: largest value, lowest index; all NaN -> 0."""
+    ok = ~np.isnan(x)
+    if not ok.any():
+        return 0
+    m = x[ok].max()
+    return int(np.flatnonzero(ok & (x == m))[0])
+
+
+@pytest.mark.parametrize("n,case", [(32000, "ties"), (32001, "tail"), (32003, "misaligned"), (65536 + 37, "rounds"),
+                                    (151936, "rounds"), (4, "tiny"), (1000, "nan"), (1000, "allneg"), (999, "allnan")])
+def test_argmax_rule(n, case):
+    """Block argmax (vector loads, several rounds, scalar tail) keeps the
+    reference's tie rule (largest value, lowest index); NaN entries never win.
+    The greedy advance uses the same routine."""
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n + 1).astype(np.float32)
+    if case == "ties":
+        x[[7, 4100, 31999]] = 9.0  # equal maxima in different threads and loads
+    elif case == "tail":
+        x[32000] = 50.0  # only the scalar tail holds it
+    elif case == "rounds":
+        x[[n - 5, n // 2]] = 11.0
+    elif case == "nan":
+        x[::3] = np.nan
+        x[500] = np.inf
+        x[600] = np.inf
+    elif case == "allneg":
+        x[:] = -np.inf
+    elif case == "allnan":
+        x[:] = np.nan
+    off = 1 if case == "misaligned" else 0  # a 4-byte offset takes the scalar path
+    buf = G.dev(x)
+    o = G.empty(4)
+    _lib.call("cpi_hip_argmax_float", ctypes.c_void_p(buf.data_ptr() + 4 * off), n, G.ptr(o), G.stream())
+    got = int(G.host(o, np.int32)[0])
+    assert got == _argmax_ref(x[off:off + n])
+    if case not in ("nan", "allnan"):
+        # the oracle restates std::max_element, which differs only on NaN
+        # (a NaN first element wins there); logits are never NaN
+        assert got == oracle.argmax(x[off:off + n])
+
+
 def test_small_ops():
     rng = np.random.default_rng(8)
     s = G.stream()
