@@ -154,6 +154,12 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     tok_s = tokens / (decode_ms / 1e3)
+    # the reference CLI's default decode: temperature 0.8, top-k 40, top-p 0.9
+    # (main_cli.cpp:12, llama_engine.hpp:74-75), sampled on device
+    eng.generate(prompt, DECODE_LEN, temperature=0.8)
+    eng.generate(prompt, DECODE_LEN, temperature=0.8)
+    s = eng.stats()
+    sampled_tok_s = s["generated_tokens"] / (s["decode_ms"] / 1e3)
     eng.close()
     log(f"[bench] decode {tokens} tok in {decode_ms:.1f} ms -> {tok_s:.1f} tok/s; prefill "
         f"{args.steps * (PROMPT_LEN - 1)} tok in {prefill_ms:.1f} ms")
@@ -193,6 +199,7 @@ def main():
                    "decode_tokens": DECODE_LEN, "prefill": "chunked MFMA (128 tokens per chunk)",
                    "parallelism": "single-gpu"},
         "prefill_tok_per_s": round(args.steps * (PROMPT_LEN - 1) / (prefill_ms / 1e3), 1),
+        "sampled_tok_per_s": round(sampled_tok_s, 1),
         "gemv_i4g32": gemv,
         "prefill_gemm_i4g32_m128": pre,
         "roofline": roof,

@@ -6,20 +6,23 @@
 // each step comes from a small device array the host fills from the same
 // generator the reference samples with (mt19937(42), one float per token).
 //
-// Thread t of 512 owns the contiguous logits [t*EPT, (t+1)*EPT) in registers
-// (EPT 64 or 128: vocabularies up to 65536).
+// Thread t of 1024 owns the contiguous logits [t*EPT, (t+1)*EPT) in registers
+// (EPT 32 or 64: vocabularies up to 65536).
 //   1. non-finite -> -inf, clamp to [-80, 80]; repetition penalty on ids set
 //      in the `seen` bitmap (the distinct history ids); no-repeat n-gram bans
 //      from the history array into an LDS bitmap.
 //   2. temperature <= 0: first maximum.
 //   3. s = l * (1/T); max over finite s.
+//   4-7 with top-k: on a compacted candidate list when it fits
+//      (samp_topk_list), with the reference's sequential sums; otherwise:
 //   4. top-k: the k-th largest s by a 4-pass MSB radix select on
 //      order-preserving 32-bit keys; s below it -> -inf (ties kept).
 //   5. p = exp(s - max) / sum.
 //   6. top-p: the largest threshold T with sum(p >= T) >= top_p, found by
 //      bisection on the bit patterns of positive floats (deterministic block
-//      sums); p < T -> 0, renormalise.  Equals the reference's sorted prefix
-//      up to the order of equal probabilities.
+//      sums); p < T -> 0, and of the p == T as many as the sorted prefix
+//      needs, lower ids first; renormalise.  This is the reference's sorted
+//      prefix, whose order of equal probabilities std::sort leaves open.
 //   7. the first id whose inclusive cumulative probability reaches r (block
 //      exclusive scan of per-thread sums), else the first most probable id.
 // Then the greedy loop's bookkeeping: *token, ring[*step % ring_len],
@@ -32,9 +35,9 @@
 
 namespace cpi {
 
-constexpr int kSampThreads = 512;
+constexpr int kSampThreads = 1024;
 constexpr int kSampWaves = kSampThreads / kWave;
-constexpr int kSampMaxVocab = kSampThreads * 128;
+constexpr int kSampMaxVocab = kSampThreads * 64;
 
 struct SampleParams {
   float temperature;
@@ -123,6 +126,227 @@ __device__ __forceinline__ float samp_exclusive_scan(float v, float* red) {
   return base + inc - v;
 }
 
+// Exclusive prefix count of one int per thread, in thread order; *total gets
+// the block sum.
+__device__ __forceinline__ int samp_exclusive_count(int v, int* red, int* total) {
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  int inc = v;
+#pragma unroll
+  for (int m = 1; m < kWave; m <<= 1) {
+    const int o = __shfl_up(inc, m, kWave);
+    if (lane >= m) inc += o;
+  }
+  if (lane == kWave - 1) red[wave] = inc;
+  __syncthreads();
+  int base = 0, all = 0;
+#pragma unroll
+  for (int w = 0; w < kSampWaves; ++w) {
+    base += w < wave ? red[w] : 0;
+    all += red[w];
+  }
+  __syncthreads();
+  *total = all;
+  return base + inc - v;
+}
+
+// Top-k candidate list, the fast path of steps 4-7 when top_k is active.
+//   a. L = the smallest over the waves of each wave's ceil(k / waves)-th
+//      largest per-thread maximum: at least k distinct elements are >= L,
+//      so the k-th largest logit is >= L too.
+//   b. The finite s >= L are compacted, in index order, into a list of at
+//      most kSampThreads entries (otherwise the caller takes the radix path).
+//   c. Entry j is kept iff fewer than k entries are greater (every greater
+//      element is >= L, hence listed): the reference's "s >= kth", ties kept.
+//   d. exp, sum, top-p over the kept entries sorted by descending probability
+//      (ties: lower id first), renormalisation and the inverse CDF are then
+//      sequential sums by one thread in the reference's order (index order,
+//      or sorted order for the top-p prefix), llama_engine_sampling_utils.cpp:
+//      127-188, so they round exactly as the CPU sampler does.
+// Returns the pick, or -1 (block-uniform) when the list would overflow.
+struct SampList {
+  alignas(16) float cv[kSampThreads];
+  int ci[kSampThreads];
+  float kp[kSampThreads];
+  int kid[kSampThreads];
+  int order[kSampThreads];
+  int keep[kSampThreads];
+  float sum;
+  int pick;
+};
+
+template <int EPT>
+__device__ int samp_topk_list(const float (&v)[EPT], int i0, int V, float mx, const SampleParams& sp, float r,
+                              SampList& sl, float* redf, int* redi) {
+  const int t = threadIdx.x;
+  const int k = sp.top_k;
+  // a.
+  float lm = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e)
+    if (i0 + e < V && isfinite(v[e])) lm = fmaxf(lm, v[e]);
+  // each wave's j-th largest thread maximum (j = ceil(k / waves), ties
+  // counted), by j rounds of wave max that retire one holder each; the
+  // minimum over the waves has at least waves * j >= k elements above it
+  const int j = (k + kSampWaves - 1) / kSampWaves;
+  if (j > kWave) return -1;
+  const int lane = t & (kWave - 1);
+  float cur = lm, wj = -INFINITY;
+  for (int q = 0; q < j; ++q) {
+    wj = wave_max(cur);
+    const uint64_t holders = __ballot(cur == wj);
+    if (holders != 0ull && lane == __ffsll(static_cast<unsigned long long>(holders)) - 1) cur = -INFINITY;
+  }
+  const float L = -samp_max(-wj, redf);
+  // b.
+  int n_own = 0;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) n_own += (i0 + e < V && isfinite(v[e]) && v[e] >= L) ? 1 : 0;
+  int n = 0;
+  int off = samp_exclusive_count(n_own, redi, &n);
+  if (n > kSampThreads) return -1;
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    if (i0 + e < V && isfinite(v[e]) && v[e] >= L) {
+      sl.cv[off] = v[e];
+      sl.ci[off] = i0 + e;
+      ++off;
+    }
+  }
+  if (t >= n && t < ((n + 3) & ~3)) sl.cv[t] = -INFINITY;  // pad for 16-byte reads
+  __syncthreads();
+  // c.
+  bool kept = false;
+  float x = 0.f;
+  if (t < n) {
+    x = sl.cv[t];
+    int greater = 0;
+    for (int m = 0; m < n; m += 4) {
+      const float4 c = *reinterpret_cast<const float4*>(&sl.cv[m]);
+      greater += (c.x > x) + (c.y > x) + (c.z > x) + (c.w > x);
+    }
+    kept = greater < k;
+  }
+  int nk = 0;
+  const int slot = samp_exclusive_count(kept ? 1 : 0, redi, &nk);
+  if (kept) {
+    sl.kp[slot] = expf(x - mx);
+    sl.kid[slot] = sl.ci[t];
+    sl.keep[slot] = 0;
+  }
+  __syncthreads();
+  if (nk <= kWave) {
+    // d. in one wave, lane s holding kept entry s: every sequential sum
+    // reads the lanes in order (readlane: no memory round trips).
+    if (t < kWave) {
+      const bool live = t < nk;
+      float x = live ? sl.kp[t] : 0.f;
+      const int id = live ? sl.kid[t] : 0;
+      auto lane_f = [](float f, int s) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), s)); };
+      float sum = 0.f;
+      for (int s = 0; s < nk; ++s) sum += lane_f(x, s);
+      int pick = 0;
+      if (sum > 0.f) {
+        float p = x / sum;
+        if (sp.top_p > 0.f && sp.top_p < 1.f) {
+          int rank = 0;
+          for (int m = 0; m < nk; ++m) {
+            const float q = lane_f(p, m);
+            rank += (q > p || (q == p && m < t)) ? 1 : 0;
+          }
+          uint64_t keep = 0ull;
+          float cs = 0.f;
+          for (int q = 0; q < nk; ++q) {
+            const int m = __ffsll(static_cast<unsigned long long>(__ballot(live && rank == q))) - 1;
+            const float pq = lane_f(p, m);
+            if (pq <= 0.f) continue;
+            keep |= 1ull << m;
+            cs += pq;
+            if (cs >= sp.top_p) break;
+          }
+          if (!((keep >> t) & 1ull)) p = 0.f;
+          float renorm = 0.f;
+          for (int s = 0; s < nk; ++s) renorm += lane_f(p, s);
+          if (renorm > 0.f) p = p / renorm;
+        }
+        float acc = 0.f;
+        pick = -1;
+        for (int s = 0; s < nk; ++s) {
+          acc += lane_f(p, s);
+          if (r <= acc) { pick = __builtin_amdgcn_readlane(id, s); break; }
+        }
+        if (pick < 0) {  // first most probable id (:187)
+          float bv = -1.f;
+          for (int s = 0; s < nk; ++s) {
+            const float q = lane_f(p, s);
+            if (q > bv) { bv = q; pick = __builtin_amdgcn_readlane(id, s); }
+          }
+        }
+      }
+      if (t == 0) sl.pick = pick;
+    }
+    __syncthreads();
+    return sl.pick;
+  }
+  // d. softmax denominator in index order (:127-136)
+  if (t == 0) {
+    float sum = 0.f;
+    for (int s = 0; s < nk; ++s) sum += sl.kp[s];
+    sl.sum = sum;
+  }
+  __syncthreads();
+  const float sum = sl.sum;
+  if (!(sum > 0.f)) return 0;
+  if (t < nk) sl.kp[t] = sl.kp[t] / sum;
+  __syncthreads();
+  const bool top_p = sp.top_p > 0.f && sp.top_p < 1.f;
+  if (top_p && t < nk) {
+    const float p = sl.kp[t];
+    int rank = 0;
+    for (int m = 0; m < nk; ++m) {
+      const float q = sl.kp[m];
+      rank += (q > p || (q == p && m < t)) ? 1 : 0;
+    }
+    sl.order[rank] = t;
+  }
+  __syncthreads();
+  if (t == 0) {
+    if (top_p) {
+      // sorted prefix until the cumulative probability reaches top_p (:141-160)
+      float cs = 0.f;
+      for (int q = 0; q < nk; ++q) {
+        const int s = sl.order[q];
+        const float p = sl.kp[s];
+        if (p <= 0.f) continue;
+        sl.keep[s] = 1;
+        cs += p;
+        if (cs >= sp.top_p) break;
+      }
+      float renorm = 0.f;
+      for (int s = 0; s < nk; ++s) {
+        if (!sl.keep[s]) sl.kp[s] = 0.f;
+        renorm += sl.kp[s];
+      }
+      if (renorm > 0.f)
+        for (int s = 0; s < nk; ++s) sl.kp[s] = sl.kp[s] / renorm;
+    }
+    // inverse CDF in index order (:176-184); ids off the list add 0
+    float acc = 0.f;
+    int pick = -1;
+    for (int s = 0; s < nk; ++s) {
+      acc += sl.kp[s];
+      if (r <= acc) { pick = sl.kid[s]; break; }
+    }
+    if (pick < 0) {  // first most probable id (:187)
+      float bv = -1.f;
+      for (int s = 0; s < nk; ++s)
+        if (sl.kp[s] > bv) { bv = sl.kp[s]; pick = sl.kid[s]; }
+    }
+    sl.pick = pick;
+  }
+  __syncthreads();
+  return sl.pick;
+}
+
 template <int EPT>
 __global__ void __launch_bounds__(kSampThreads) sample_advance_kernel(
     const float* logits, int V, SampleParams sp, const float* rand, int rand_len, uint32_t* seen, int* history,
@@ -132,6 +356,7 @@ __global__ void __launch_bounds__(kSampThreads) sample_advance_kernel(
   __shared__ int redi[kSampWaves];
   __shared__ uint32_t hist[256];
   __shared__ uint32_t sel_prefix, sel_k;
+  __shared__ SampList slist;
 
   const int t = threadIdx.x;
   const int i0 = t * EPT;
@@ -156,18 +381,41 @@ __global__ void __launch_bounds__(kSampThreads) sample_advance_kernel(
     __syncthreads();
   }
 
+  // The thread's EPT logits as 16-byte loads (i0 is a multiple of 32) and
+  // its EPT/32 words of the seen / ban bitmaps, each word loaded once.
   float v[EPT];
+  if (i0 + EPT <= V && (reinterpret_cast<uintptr_t>(logits) & 15u) == 0) {
+    const float4* l4 = reinterpret_cast<const float4*>(logits + i0);
+#pragma unroll
+    for (int q = 0; q < EPT / 4; ++q) {
+      const float4 f = l4[q];
+      v[4 * q] = f.x;
+      v[4 * q + 1] = f.y;
+      v[4 * q + 2] = f.z;
+      v[4 * q + 3] = f.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) v[e] = i0 + e < V ? logits[i0 + e] : 0.f;
+  }
+  const bool rep = sp.rep_penalty > 1.f && seen;
+  uint32_t sw[EPT / 32], bw[EPT / 32];
+#pragma unroll
+  for (int w = 0; w < EPT / 32; ++w) {
+    const bool in = i0 + 32 * w < V;
+    sw[w] = (rep && in) ? seen[i0 / 32 + w] : 0u;
+    bw[w] = (ngram && in) ? ban[i0 / 32 + w] : 0u;
+  }
   bool cand = false;
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const int i = i0 + e;
     float x = -INFINITY;
     if (i < V) {
-      x = logits[i];
+      x = v[e];
       x = isfinite(x) ? fminf(fmaxf(x, -80.f), 80.f) : -INFINITY;
-      if (sp.rep_penalty > 1.f && seen && ((seen[i >> 5] >> (i & 31)) & 1u))
-        x = x > 0.f ? x / sp.rep_penalty : x * sp.rep_penalty;
-      if (ngram && ((ban[i >> 5] >> (i & 31)) & 1u)) x = -INFINITY;
+      if ((sw[e >> 5] >> (e & 31)) & 1u) x = x > 0.f ? x / sp.rep_penalty : x * sp.rep_penalty;
+      if ((bw[e >> 5] >> (e & 31)) & 1u) x = -INFINITY;
       cand |= isfinite(x);
     }
     v[e] = x;
@@ -196,6 +444,11 @@ __global__ void __launch_bounds__(kSampThreads) sample_advance_kernel(
     if (!isfinite(mx)) {
       pick = 0;
     } else {
+      // ---- 4-7 on the top-k candidate list when it fits
+      if (sp.top_k > 0 && sp.top_k < V)
+        pick = samp_topk_list<EPT>(v, i0, V, mx, sp, rand[st % rand_len], slist, redf, redi);
+    }
+    if (pick < 0 && isfinite(mx)) {
       // ---- 4. top-k: k-th largest key, MSB-first radix select
       if (sp.top_k > 0 && sp.top_k < V) {
         if (t == 0) {
@@ -262,10 +515,37 @@ __global__ void __launch_bounds__(kSampThreads) sample_advance_kernel(
             else hi = mid - 1u;
           }
           const float thr = __uint_as_float(lo);
+          // Probabilities equal to thr are taken in id order, as many as the
+          // sorted prefix needs to reach top_p (the reference's order of
+          // equal probabilities is unspecified; lower ids first, as the
+          // candidate list and the CPU oracle do).
+          float gt = 0.f;
+          int nt = 0;
+#pragma unroll
+          for (int e = 0; e < EPT; ++e) {
+            gt += v[e] > thr ? v[e] : 0.f;
+            nt += v[e] == thr ? 1 : 0;
+          }
+          const float s_gt = samp_sum(gt, redf);
+          int ties = 0;
+          int tie_rank = samp_exclusive_count(nt, redi, &ties);
+          if (t == 0) {
+            float cs = s_gt;
+            int c = 0;
+            while (c < ties && cs < sp.top_p) {
+              cs += thr;
+              ++c;
+            }
+            sel_k = static_cast<uint32_t>(c);
+          }
+          __syncthreads();
+          const int take = static_cast<int>(sel_k);
           float kept = 0.f;
 #pragma unroll
           for (int e = 0; e < EPT; ++e) {
-            v[e] = v[e] >= thr ? v[e] : 0.f;
+            bool keep = v[e] > thr;
+            if (v[e] == thr) keep = tie_rank++ < take;
+            v[e] = keep ? v[e] : 0.f;
             kept += v[e];
           }
           const float renorm = samp_sum(kept, redf);
@@ -314,11 +594,11 @@ hipError_t sample_advance_launch(const float* logits, int V, const SampleParams&
                                  uint32_t* seen, int* history, int hist_cap, int* token, int* position, int* step,
                                  int* ring, int ring_len, hipStream_t s) {
   const dim3 g(1), b(kSampThreads);
-  if (V <= kSampThreads * 64)
-    hipLaunchKernelGGL(sample_advance_kernel<64>, g, b, 0, s, logits, V, sp, rand, rand_len, seen, history,
+  if (V <= kSampThreads * 32)
+    hipLaunchKernelGGL(sample_advance_kernel<32>, g, b, 0, s, logits, V, sp, rand, rand_len, seen, history,
                        hist_cap, token, position, step, ring, ring_len);
   else if (V <= kSampMaxVocab)
-    hipLaunchKernelGGL(sample_advance_kernel<128>, g, b, 0, s, logits, V, sp, rand, rand_len, seen, history,
+    hipLaunchKernelGGL(sample_advance_kernel<64>, g, b, 0, s, logits, V, sp, rand, rand_len, seen, history,
                        hist_cap, token, position, step, ring, ring_len);
   else
     return hipErrorInvalidValue;

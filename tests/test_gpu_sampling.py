@@ -150,3 +150,52 @@ def test_sample_rejects_bad_args():
     assert L.cpi_hip_sample_advance(*args) == -1  # vocab too large
     args[1], args[4] = 100, 0
     assert L.cpi_hip_sample_advance(*args) == -1  # rand_len
+
+
+def _topk_edge_logits(name):
+    rng = np.random.default_rng(7)
+    V = 32000
+    if name == "levels":  # few distinct values: ties at the k-th value and in the top-p prefix
+        return (np.round(rng.standard_normal(V) * 2) / 2).astype(np.float32)
+    if name == "list_overflow":  # 1100 tied maxima > the 1024-entry candidate list: radix path
+        lg = np.full(V, -5.0, np.float32)
+        lg[rng.choice(V, 1100, replace=False)] = 2.0
+        return lg
+    if name == "few_finite":  # fewer finite logits than k
+        lg = np.full(V, -np.inf, np.float32)
+        lg[rng.choice(V, 10, replace=False)] = rng.standard_normal(10).astype(np.float32)
+        return lg
+    if name == "clustered":  # the k largest inside one thread's 64 contiguous ids
+        lg = (rng.standard_normal(V)).astype(np.float32)
+        lg[12800:12864] = 6.0 + rng.standard_normal(64).astype(np.float32)
+        return lg
+    raise ValueError(name)
+
+
+@pytest.mark.parametrize("name", ["levels", "list_overflow", "few_finite", "clustered"])
+@pytest.mark.parametrize("top_k,top_p", [(40, 0.9), (1, 1.0), (5, 0.5), (256, 0.95), (0, 0.9)])
+def test_sample_topk_list_edges(name, top_k, top_p):
+    """Top-k candidate list (lower bound from per-thread maxima, compacted
+    list, exact ranks), its fallback to the radix select, and the top-p
+    bisection without top-k; ties at the top-k and top-p boundaries."""
+    print(f"[sample-topk] case={name} k={top_k} p={top_p}", flush=True)
+    lg = _topk_edge_logits(name)
+    params = _lib.SamplingParams(0.9, top_k, top_p, 1.0, 0)
+    p = f64_probs(lg, 0.9, top_k, top_p)
+    rng = np.random.default_rng(top_k)
+    picks = set()
+    for r in safe_draws(p, 8, rng):
+        got = run(lg, params, r)[0]
+        picks.add(got)
+        assert p[got] > 0
+        if top_k == 0:
+            # thousands of kept ids: float32 cumulative sums in block order
+            # drift from the sequential ones by more than the draw margin,
+            # so the pick is checked against the float64 CDF with 1e-3 slack
+            cum = np.cumsum(p)
+            assert cum[got] - p[got] - 1e-3 <= r <= cum[got] + 1e-3, (r, got)
+            continue
+        want = oracle.sample(lg, 0.9, top_k, top_p, 1.0, 0, [], r)
+        assert got == want, (r, got, want)
+    if name == "list_overflow" and top_k == 40:
+        assert len(picks) > 1  # all 1100 tied ids stay candidates
