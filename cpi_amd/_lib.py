@@ -110,6 +110,7 @@ _SIGS = {
     "cpi_hip_moe_combine": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_void_p]),
     "cpi_hip_argmax_float": (c_int, [c_void_p, c_int, c_void_p, c_void_p]),
     "cpi_hip_greedy_advance": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_void_p]),
+    "cpi_hip_greedy_advance_embed": (c_int, [c_void_p, c_int, c_void_p, c_int] + [c_void_p] * 5 + [c_int, c_void_p]),
     "cpi_hip_prompt_advance": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p]),
     "cpi_hip_quantize_rowwise_fp16_to_int8": (c_int, [c_void_p] * 3 + [c_int, c_int, c_int, c_void_p]),
     "cpi_hip_pack_rowwise_int8_to_int4": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p]),

@@ -427,8 +427,22 @@ int cpi_hip_greedy_advance(const float* logits, int n, int* token, int* position
   if (!logits || n <= 0 || !token || !position || !step || !ring || ring_len <= 0)
     return fail("greedy_advance: bad arguments");
   hipLaunchKernelGGL(cpi::argmax_advance_kernel, dim3(1), dim3(1024), 0, S(s), logits, n, token,
-                     position, step, ring, ring_len);
+                     position, step, ring, ring_len, static_cast<const uint16_t*>(nullptr), 0,
+                     static_cast<float*>(nullptr));
   return check(hipGetLastError(), "greedy_advance");
+}
+
+int cpi_hip_greedy_advance_embed(const float* logits, int n, const uint16_t* embedding, int hidden, float* x_out,
+                                 int* token, int* position, int* step, int* ring, int ring_len, cpi_stream_t s) {
+  if (!logits || n <= 0 || !embedding || !x_out || !token || !position || !step || !ring || ring_len <= 0)
+    return fail("greedy_advance_embed: bad arguments");
+  if (hidden <= 0 || (hidden & 3) || (reinterpret_cast<uintptr_t>(embedding) & 7) ||
+      (reinterpret_cast<uintptr_t>(x_out) & 15))
+    return fail("greedy_advance_embed: hidden must be a positive multiple of 4, embedding 8-byte and x_out "
+                "16-byte aligned");
+  hipLaunchKernelGGL(cpi::argmax_advance_kernel, dim3(1), dim3(1024), 0, S(s), logits, n, token,
+                     position, step, ring, ring_len, embedding, hidden, x_out);
+  return check(hipGetLastError(), "greedy_advance_embed");
 }
 
 int cpi_hip_sample_advance(const float* logits, int vocab, const cpi_sampling_params* params, const float* rand,

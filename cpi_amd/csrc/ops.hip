@@ -315,12 +315,26 @@ __global__ void __launch_bounds__(1024) argmax_kernel(const float* x, int n, int
 // the next input token, is appended to the output ring at *step, and the
 // position/step counters advance (replaces argmax + copy_int + increment_int,
 // llama_engine_graph.cpp:472-474).
+// With emb != nullptr it also writes the next step's input, emb[token] as
+// fp32, to x_out [hidden] (hidden a multiple of 4, emb 8-byte aligned), so
+// the next step starts without an embedding launch.
 __global__ void __launch_bounds__(1024) argmax_advance_kernel(const float* x, int n, int* token,
                                                               int* position, int* step,
-                                                              int* ring, int ring_len) {
+                                                              int* ring, int ring_len,
+                                                              const uint16_t* emb, int hidden,
+                                                              float* x_out) {
   float v;
   int i;
   block_argmax(x, n, v, i);
+  if (emb != nullptr) {
+    const uint2* row = reinterpret_cast<const uint2*>(emb + static_cast<size_t>(i) * hidden);
+    for (int q = threadIdx.x; q < hidden / 4; q += blockDim.x) {
+      const uint2 h = row[q];
+      const f16x2 a = as_h2(h.x), b = as_h2(h.y);
+      reinterpret_cast<f32x4*>(x_out)[q] =
+          f32x4{static_cast<float>(a.x), static_cast<float>(a.y), static_cast<float>(b.x), static_cast<float>(b.y)};
+    }
+  }
   if (threadIdx.x == 0) {
     *token = i;
     const int s = *step;

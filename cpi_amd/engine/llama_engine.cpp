@@ -505,7 +505,10 @@ void LlamaEngine::enqueue_step(bool with_head, const cpi_sampling_params* sampli
     CPI_OK(cpi_hip_decode_step_fused(&fused_desc_, stream_));
     return;
   }
-  CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_token_, x_, 1, H, stream_));
+  // A greedy step's input embedding was written by the previous step's tail
+  // (or before the first decode step); the others look it up here.
+  const bool greedy_step = with_head && !sampling;
+  if (!greedy_step) CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_token_, x_, 1, H, stream_));
   // MoE layers leave their expert outputs (moe_y_, weights d_moe_prob_) to be
   // folded into the next consumer's prologue, which writes the updated
   // residual to the other buffer of the x_ / x2_ pair.
@@ -598,8 +601,8 @@ void LlamaEngine::enqueue_step(bool with_head, const cpi_sampling_params* sampli
       CPI_OK(cpi_hip_sample_advance(logits_, cfg_.vocab_size, sampling, d_rand_, rand_len_, d_seen_, d_hist_,
                                     opts_.max_context, d_token_, d_pos_, d_step_, d_ring_, ring_len_, stream_));
     else
-      CPI_OK(cpi_hip_greedy_advance(logits_, cfg_.vocab_size, d_token_, d_pos_, d_step_, d_ring_, ring_len_,
-                                    stream_));
+      CPI_OK(cpi_hip_greedy_advance_embed(logits_, cfg_.vocab_size, emb_, H, x_, d_token_, d_pos_, d_step_, d_ring_,
+                                          ring_len_, stream_));
   } else {
     CPI_OK(cpi_hip_prompt_advance(d_prompt_, prompt_cap_, d_token_, d_pos_, stream_));
   }
@@ -764,6 +767,9 @@ std::vector<int> LlamaEngine::generate_stream(const std::vector<int>& prompt_in,
     sp.no_repeat_ngram_size = opts_.no_repeat_ngram_size;
     ensure_sample_graphs(sp);
   }
+  // greedy graphs expect the step's input embedding in x_ (their tails keep
+  // it there for the next step)
+  if (greedy && !fused_) CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_token_, x_, 1, cfg_.hidden_size, stream_));
   const bool capture_logits = capture_ != nullptr && capture_steps_ > 0;
   std::vector<int> ring(static_cast<std::size_t>(ring_len_));
   std::vector<int> history = out;

@@ -436,6 +436,14 @@ int cpi_hip_argmax_float(const float* logits, int n, int* out_index,
  * src/engine/llama_engine_graph.cpp:472-474. */
 int cpi_hip_greedy_advance(const float* logits, int n, int* token, int* position,
                            int* step, int* ring, int ring_len, cpi_stream_t stream);
+/* cpi_hip_greedy_advance, then the next step's input: x_out[0:hidden] =
+ * embedding[token] as fp32 (hidden a multiple of 4).  Folds the embedding
+ * lookup at the head of the next captured step (launch_embedding_lookup,
+ * kernels.cuh:82-87, src/engine/llama_engine_graph.cpp:604) into the
+ * step tail at src/engine/llama_engine_graph.cpp:472-474. */
+int cpi_hip_greedy_advance_embed(const float* logits, int n, const uint16_t* embedding,
+                                 int hidden, float* x_out, int* token, int* position,
+                                 int* step, int* ring, int ring_len, cpi_stream_t stream);
 /* On-device sampling step, replacing the logits graph's host round trip
  * (src/engine/llama_engine_graph.cpp:818-837: all V logits copied to the host
  * per token) and the host sampler it feeds

@@ -528,3 +528,32 @@ def test_router_topk_matches_oracle_exactly(case):
     np.testing.assert_allclose(G.host(pr, np.float32, k), rpr, rtol=1e-6, atol=1e-7)
     if case == "ties":
         assert list(ridx) == [1, 2, 4]
+
+
+@pytest.mark.parametrize("V,H", [(32000, 4096), (1000, 68), (151936, 2048)])
+def test_greedy_advance_embed(V, H):
+    """Greedy tail with the next step's embedding: token/ring/step/position as
+    cpi_hip_greedy_advance, and x_out = the token's embedding row as fp32,
+    bit-exact (fp16 -> fp32 is exact)."""
+    rng = np.random.default_rng(V)
+    lg = rng.standard_normal(V).astype(np.float32)
+    lg[[V // 3, V - 2]] = 7.5  # tie: the lower id wins
+    emb = (rng.standard_normal((V, H)) * 0.02).astype(np.float16)
+    d_lg, d_emb = G.dev(lg), G.dev(emb.view(np.uint16))
+    x = G.dev(np.full(H + 4, -1.0, np.float32))
+    state = G.dev(np.array([0, 41, 5], np.int32))  # token, position, step
+    ring = G.dev(np.full(4, -1, np.int32))
+    b = state.data_ptr()
+    _lib.call("cpi_hip_greedy_advance_embed", G.ptr(d_lg), V, G.ptr(d_emb), H, G.ptr(x), ctypes.c_void_p(b),
+              ctypes.c_void_p(b + 4), ctypes.c_void_p(b + 8), G.ptr(ring), 4, G.stream())
+    tok, pos, step = (int(v) for v in G.host(state, np.int32, 3))
+    want = V // 3
+    assert (tok, pos, step) == (want, 42, 6)
+    assert G.host(ring, np.int32, 4)[5 % 4] == want
+    out = G.host(x, np.float32, H + 4)
+    np.testing.assert_array_equal(out[:H], emb[want].astype(np.float32))
+    assert (out[H:] == -1.0).all()  # nothing past hidden
+    L = _lib.lib()
+    assert L.cpi_hip_greedy_advance_embed(G.ptr(d_lg), V, G.ptr(d_emb), H + 2, G.ptr(x), ctypes.c_void_p(b),
+                                          ctypes.c_void_p(b + 4), ctypes.c_void_p(b + 8), G.ptr(ring), 4,
+                                          G.stream()) == -1  # hidden not a multiple of 4
