@@ -350,7 +350,8 @@ __device__ int samp_topk_list(const float (&v)[EPT], int i0, int V, float mx, co
 template <int EPT>
 __global__ void __launch_bounds__(kSampThreads) sample_advance_kernel(
     const float* logits, int V, SampleParams sp, const float* rand, int rand_len, uint32_t* seen, int* history,
-    int hist_cap, int* token, int* position, int* step, int* ring, int ring_len) {
+    int hist_cap, int* token, int* position, int* step, int* ring, int ring_len, const uint16_t* emb, int hidden,
+    float* x_out) {
   __shared__ uint32_t ban[kSampMaxVocab / 32];
   __shared__ float redf[kSampWaves];
   __shared__ int redi[kSampWaves];
@@ -580,6 +581,16 @@ __global__ void __launch_bounds__(kSampThreads) sample_advance_kernel(
     }
   }
 
+  // the next step's input, emb[pick] as fp32 (pick is block-uniform here)
+  if (emb != nullptr) {
+    const uint2* row = reinterpret_cast<const uint2*>(emb + static_cast<size_t>(pick) * hidden);
+    for (int q = t; q < hidden / 4; q += kSampThreads) {
+      const uint2 h = row[q];
+      const f16x2 a = as_h2(h.x), b = as_h2(h.y);
+      reinterpret_cast<f32x4*>(x_out)[q] =
+          f32x4{static_cast<float>(a.x), static_cast<float>(a.y), static_cast<float>(b.x), static_cast<float>(b.y)};
+    }
+  }
   if (t == 0) {
     *token = pick;
     ring[st % ring_len] = pick;
@@ -592,14 +603,15 @@ __global__ void __launch_bounds__(kSampThreads) sample_advance_kernel(
 
 hipError_t sample_advance_launch(const float* logits, int V, const SampleParams& sp, const float* rand, int rand_len,
                                  uint32_t* seen, int* history, int hist_cap, int* token, int* position, int* step,
-                                 int* ring, int ring_len, hipStream_t s) {
+                                 int* ring, int ring_len, const uint16_t* emb, int hidden, float* x_out,
+                                 hipStream_t s) {
   const dim3 g(1), b(kSampThreads);
   if (V <= kSampThreads * 32)
     hipLaunchKernelGGL(sample_advance_kernel<32>, g, b, 0, s, logits, V, sp, rand, rand_len, seen, history,
-                       hist_cap, token, position, step, ring, ring_len);
+                       hist_cap, token, position, step, ring, ring_len, emb, hidden, x_out);
   else if (V <= kSampMaxVocab)
     hipLaunchKernelGGL(sample_advance_kernel<64>, g, b, 0, s, logits, V, sp, rand, rand_len, seen, history,
-                       hist_cap, token, position, step, ring, ring_len);
+                       hist_cap, token, position, step, ring, ring_len, emb, hidden, x_out);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

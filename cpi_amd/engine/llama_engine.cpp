@@ -505,10 +505,10 @@ void LlamaEngine::enqueue_step(bool with_head, const cpi_sampling_params* sampli
     CPI_OK(cpi_hip_decode_step_fused(&fused_desc_, stream_));
     return;
   }
-  // A greedy step's input embedding was written by the previous step's tail
-  // (or before the first decode step); the others look it up here.
-  const bool greedy_step = with_head && !sampling;
-  if (!greedy_step) CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_token_, x_, 1, H, stream_));
+  // A decode step's input embedding was written by the previous step's tail
+  // (or before the first decode step); prompt steps look it up here.
+  const bool tail_embeds = with_head;
+  if (!tail_embeds) CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_token_, x_, 1, H, stream_));
   // MoE layers leave their expert outputs (moe_y_, weights d_moe_prob_) to be
   // folded into the next consumer's prologue, which writes the updated
   // residual to the other buffer of the x_ / x2_ pair.
@@ -598,8 +598,9 @@ void LlamaEngine::enqueue_step(bool with_head, const cpi_sampling_params* sampli
     fold(h, false);
     CPI_OK(cpi_hip_gemv(&h, stream_));
     if (sampling)
-      CPI_OK(cpi_hip_sample_advance(logits_, cfg_.vocab_size, sampling, d_rand_, rand_len_, d_seen_, d_hist_,
-                                    opts_.max_context, d_token_, d_pos_, d_step_, d_ring_, ring_len_, stream_));
+      CPI_OK(cpi_hip_sample_advance_embed(logits_, cfg_.vocab_size, sampling, d_rand_, rand_len_, d_seen_, d_hist_,
+                                          opts_.max_context, emb_, H, x_, d_token_, d_pos_, d_step_, d_ring_,
+                                          ring_len_, stream_));
     else
       CPI_OK(cpi_hip_greedy_advance_embed(logits_, cfg_.vocab_size, emb_, H, x_, d_token_, d_pos_, d_step_, d_ring_,
                                           ring_len_, stream_));
@@ -767,9 +768,10 @@ std::vector<int> LlamaEngine::generate_stream(const std::vector<int>& prompt_in,
     sp.no_repeat_ngram_size = opts_.no_repeat_ngram_size;
     ensure_sample_graphs(sp);
   }
-  // greedy graphs expect the step's input embedding in x_ (their tails keep
-  // it there for the next step)
-  if (greedy && !fused_) CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_token_, x_, 1, cfg_.hidden_size, stream_));
+  // the per-op decode graphs expect the step's input embedding in x_ (their
+  // tails keep it there for the next step); the fused step looks it up itself
+  const bool per_op = dev_sample || !fused_;
+  if (per_op) CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_token_, x_, 1, cfg_.hidden_size, stream_));
   const bool capture_logits = capture_ != nullptr && capture_steps_ > 0;
   std::vector<int> ring(static_cast<std::size_t>(ring_len_));
   std::vector<int> history = out;
@@ -800,8 +802,13 @@ std::vector<int> LlamaEngine::generate_stream(const std::vector<int>& prompt_in,
                          static_cast<std::size_t>(cfg_.vocab_size) * 4, hipMemcpyDeviceToHost));
     } else {
       HIP_OK(hipStreamSynchronize(stream_));
+      if (capture_logits && step < capture_steps_)
+        HIP_OK(hipMemcpy(capture_ + static_cast<std::size_t>(step) * cfg_.vocab_size, logits_,
+                         static_cast<std::size_t>(cfg_.vocab_size) * 4, hipMemcpyDeviceToHost));
       ids[0] = sample_host(temperature, history);
       HIP_OK(hipMemcpyAsync(d_token_, ids, 4, hipMemcpyHostToDevice, stream_));
+      // the greedy tail embedded its own pick: the next step needs this one
+      if (per_op) CPI_OK(cpi_hip_embedding_lookup_f32(emb_, d_token_, x_, 1, cfg_.hidden_size, stream_));
     }
     for (int i = 0; i < n && !stop; ++i) {
       const int tok = (greedy || dev_sample) ? ring[static_cast<std::size_t>((step) % ring_len_)] : ids[0];

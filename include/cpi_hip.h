@@ -469,6 +469,16 @@ int cpi_hip_sample_advance(const float* logits, int vocab, const cpi_sampling_pa
                            const float* rand, int rand_len, uint32_t* seen, int* history,
                            int history_cap, int* token, int* position, int* step, int* ring,
                            int ring_len, cpi_stream_t stream);
+/* cpi_hip_sample_advance, then the next step's input: x_out[0:hidden] =
+ * embedding[token] as fp32 (hidden a multiple of 4).  Folds the embedding
+ * lookup at the head of the next step (launch_embedding_lookup,
+ * kernels.cuh:82-87, src/engine/llama_engine_graph.cpp:604) into the
+ * sampling step tail. */
+int cpi_hip_sample_advance_embed(const float* logits, int vocab, const cpi_sampling_params* params,
+                                 const float* rand, int rand_len, uint32_t* seen, int* history,
+                                 int history_cap, const uint16_t* embedding, int hidden, float* x_out,
+                                 int* token, int* position, int* step, int* ring, int ring_len,
+                                 cpi_stream_t stream);
 /* Prompt step tail (sequential prefill inside a graph): ++*position, then
  * token = prompt[*position] when *position < n_prompt.  Replaces the host
  * token/position copies of the per-token prefill loop

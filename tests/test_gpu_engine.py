@@ -258,6 +258,8 @@ SAMPLE_CASES = {
     "T0.8_k40_p0.9": dict(temperature=0.8, top_k=40, top_p=0.9, rep=1.0, ngram=0),
     "T1.0_rep1.2_ngram3": dict(temperature=1.0, top_k=0, top_p=1.0, rep=1.2, ngram=3),
     "T0_rep1.3": dict(temperature=0.0, top_k=40, top_p=0.9, rep=1.3, ngram=0),
+    # beyond the device sampler's 65536 ids: the host sampler after each step
+    "V70000_host_T0.8_k40_p0.9": dict(temperature=0.8, top_k=40, top_p=0.9, rep=1.1, ngram=0, vocab=70000),
 }
 
 
@@ -271,7 +273,7 @@ def test_sampled_decode_matches_oracle(tmp_path, name):
     from tests.test_gpu_sampling import f64_probs
     kw = SAMPLE_CASES[name]
     print(f"[engine] sampled case={name}", flush=True)
-    cfg = tiny_cfg()
+    cfg = tiny_cfg(vocab_size=kw.get("vocab", 1000))
     path = str(tmp_path / "s.ll2c")
     ll2c.write_synthetic(path, ll2c.SynthSpec(cfg, attn_fmt="i4g32", mlp_fmt="i4g32", seed=5, std=0.02,
                                               norm_jitter=0.1))
