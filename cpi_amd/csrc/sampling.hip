@@ -363,6 +363,9 @@ __global__ void __launch_bounds__(kSampThreads) sample_advance_kernel(
   const int i0 = t * EPT;
   const int pos = *position;
   const int st = *step;
+  // the step's uniform draw, requested up front rather than after the
+  // reductions that precede its use
+  const float r_draw = rand[st % rand_len];
   const int hist_len = history ? min(pos + 1, hist_cap) : 0;
 
   // ---- 1. n-gram bans (llama_engine_sampling_utils.cpp:55-94)
@@ -447,7 +450,7 @@ __global__ void __launch_bounds__(kSampThreads) sample_advance_kernel(
     } else {
       // ---- 4-7 on the top-k candidate list when it fits
       if (sp.top_k > 0 && sp.top_k < V)
-        pick = samp_topk_list<EPT>(v, i0, V, mx, sp, rand[st % rand_len], slist, redf, redi);
+        pick = samp_topk_list<EPT>(v, i0, V, mx, sp, r_draw, slist, redf, redi);
     }
     if (pick < 0 && isfinite(mx)) {
       // ---- 4. top-k: k-th largest key, MSB-first radix select
@@ -556,7 +559,7 @@ __global__ void __launch_bounds__(kSampThreads) sample_advance_kernel(
           }
         }
         // ---- 7. inverse CDF at r
-        const float r = rand[st % rand_len];
+        const float r = r_draw;
         float own = 0.f;
 #pragma unroll
         for (int e = 0; e < EPT; ++e) own += v[e];
